@@ -1,0 +1,162 @@
+/* C ABI of libmoe_gfx950.so — the gfx950 (MI355X) MoE expert pipeline.
+ *
+ * Every entry point takes plain device pointers, element counts and a hipStream_t passed as
+ * `void* stream` (NULL = the default stream). Nothing here allocates: the caller owns every
+ * buffer, including the dispatch workspace. Calls are stream-ordered and asynchronous; none of
+ * them synchronises with the host. Each returns MOE_OK or one of the MOE_ERR_* codes below; a
+ * failed call launches nothing.
+ *
+ * Shapes (reference layout, /root/reference/kernels/sm75/moe.py:65-68):
+ *   hidden         (N, H)        row-major, dtype = the model dtype
+ *   top_k_indices  (N, k)        int64 expert ids
+ *   top_k_weights  (N, k)        model dtype
+ *   gate_up_proj   (E_glu, 2I, H) rows [0, I) = gate, rows [I, 2I) = up
+ *   down_proj      (E_glu, H, I)
+ *   act_codes      (E,) int32    E = E_glu + number of weightless special experts
+ * M = N*k routed rows. "Sorted" rows are ordered by (expert id, flat index t*k+j): stable.
+ */
+#ifndef MOE_GFX950_H
+#define MOE_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_OK 0
+#define MOE_ERR_SHAPE 1     /* a size is out of range or inconsistent */
+#define MOE_ERR_ALIGN 2     /* a pointer or row length breaks the 16-byte rule */
+#define MOE_ERR_CODE 3      /* an activation code the entry point does not implement */
+#define MOE_ERR_DTYPE 4     /* unknown dtype code */
+#define MOE_ERR_LAUNCH 5    /* the HIP launch itself failed */
+#define MOE_ERR_WORKSPACE 6 /* workspace missing or too small */
+
+#define MOE_DT_F32 0
+#define MOE_DT_F16 1
+#define MOE_DT_BF16 2
+
+/* Library version string. */
+const char* moe_version(void);
+
+/* Rows per token tile of the grouped GEMMs; tile_offsets below count tiles of this height. */
+int moe_tile_rows(void);
+
+/* Bytes of device workspace moe_dispatch needs. */
+size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_experts);
+
+/* Dispatch: histogram, prefix scan and stable permutation of the routed rows.
+ * Replaces `_sort_by_expert` (kernels/sm75/moe.py:564-572), `_build_schedule` (:535-543) and the
+ * sort / bincount / cumsum of kernels/sm120/moe_grouped.py:94-100, with no host sync.
+ * Outputs: counts[E], offsets[E+1] (exclusive prefix of counts), tile_offsets[E+1] (exclusive
+ * prefix of ceil(counts/moe_tile_rows())), sorted_token[M] (token id t of each sorted row),
+ * sorted_flat[M] (flat index t*k+j of each sorted row), flat_to_sorted[M] (inverse permutation;
+ * -1 for an index outside [0, E)), status[0] += number of such out-of-range indices. */
+int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int n_experts,
+                 int32_t* counts, int32_t* offsets, int32_t* tile_offsets, int32_t* sorted_token,
+                 int32_t* sorted_flat, int32_t* flat_to_sorted, int32_t* status, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* Grouped gate/up projection with the GLU epilogue.
+ * gate_up[m] = hidden[sorted_token[m]] @ gate_up_proj[e]^T for every sorted row m of a GLU expert
+ * e < E_glu; inter[m, i] = act_e(gate) * up (act code 0 = SiLU, 1 = ReLU^2; the two codes the
+ * epilogue fuses). inter_out may be NULL: then only gate_up is written (any act code).
+ * Replaces `_grouped_mm` + `_glu_fwd` (kernels/sm75/moe.py:590-591), torch._grouped_mm +
+ * BatchedGLU (kernels/sm120/moe_grouped.py:106-107) and the per-expert `@` + `_glu_fwd`
+ * (kernels/sm75/moe.py:765-769). */
+int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int64_t n_tokens, int64_t H,
+                                  const void* gate_up_proj, int E_glu, int64_t I,
+                                  const int32_t* act_codes, const int32_t* offsets,
+                                  const int32_t* tile_offsets, const int32_t* sorted_token,
+                                  int64_t n_rows, void* gate_up_out, void* inter_out, void* stream);
+
+/* Grouped down projection: eo[m] = inter[m] @ down_proj[e]^T.
+ * Replaces `_grouped_mm(inter, down_proj, ...)` (kernels/sm75/moe.py:592), the per-expert
+ * `it @ down_proj[e].t()` (:770) and torch._grouped_mm (kernels/sm120/moe_grouped.py:108). */
+int moe_grouped_down_fwd(int dtype, const void* inter, const void* down_proj, int E_glu, int64_t H,
+                         int64_t I, const int32_t* offsets, const int32_t* tile_offsets,
+                         int64_t n_rows, void* eo_out, void* stream);
+
+/* Gate-weighted combine: out[t] = sum_j w[t,j] * row(t,j), fp32 accumulation in slot order, where
+ * row = eo[flat_to_sorted[t*k+j]] for GLU experts, hidden[t] for Identity (code 3), nothing for
+ * Zero (code 4); experts e >= E_glu are the weightless specials, n_experts = len(act_codes).
+ * Replaces `_combine_scatter` (kernels/sm75/moe.py:673-682,704-709), the grouped
+ * index_add_ (:593-595) and kernels/sm120/moe_grouped.py:110-121. Deterministic (no atomics). */
+int moe_combine_fwd(int dtype, const void* eo, const void* hidden, const void* top_k_weights,
+                    const int64_t* top_k_indices, const int32_t* act_codes, int n_experts, int E_glu,
+                    const int32_t* flat_to_sorted, int64_t n_tokens, int top_k, int64_t H,
+                    void* out, void* stream);
+
+/* Combine backward: grad_eo[m] = grad_out[t] * w (GLU rows), grad_wt[flat] = sum_h grad_out[t,h] *
+ * row[h] (fp32 reduction; row = eo[m] for GLU, hidden[t] for Identity, 0 for Zero).
+ * grad_out rows are `grad_out_ld` elements apart. Replaces `_combine_bwd`
+ * (kernels/sm75/moe.py:688-701,712-720) and the grouped bwd prologue (:606-608,616-617). */
+int moe_combine_bwd(int dtype, const void* grad_out, int64_t grad_out_ld, const void* eo,
+                    const void* hidden, const void* top_k_weights, const int64_t* top_k_indices,
+                    const int32_t* act_codes, int n_experts, int E_glu, const int32_t* sorted_token,
+                    const int32_t* sorted_flat, int64_t n_rows, int top_k, int64_t H,
+                    void* grad_eo_out, void* grad_wt_out, void* stream);
+
+/* Down-projection dX with the GLU-backward epilogue:
+ * grad_inter[m] = grad_eo[m] @ down_proj[e]; ggu[m] = [d gate, d up] of act_e(gate)*up.
+ * grad_inter_out may be NULL; when it is given (any act code) grad_inter is written and ggu_out
+ * may be NULL. Replaces `_grouped_mm(..., trans_w=True)` + `_glu_bwd` (kernels/sm75/moe.py:609-611)
+ * and the per-expert `ge @ down_proj[e]` + `_glu_bwd` (:807,817-819). */
+int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo, const void* down_proj, int E_glu,
+                                   int64_t H, int64_t I, const void* gate_up,
+                                   const int32_t* act_codes, const int32_t* offsets,
+                                   const int32_t* tile_offsets, int64_t n_rows, void* ggu_out,
+                                   void* grad_inter_out, void* stream);
+
+/* Gate/up dX: grad_x_s[m] = ggu[m] @ gate_up_proj[e]. Replaces `_grouped_mm(grad_gate_up,
+ * gate_up_proj, ..., trans_w=True)` (kernels/sm75/moe.py:612) and `grad_gate_up @
+ * gate_up_proj[e]` (:822). */
+int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj, int E_glu, int64_t H,
+                          int64_t I, const int32_t* offsets, const int32_t* tile_offsets,
+                          int64_t n_rows, void* grad_xs_out, void* stream);
+
+/* Grouped weight gradient over each expert's ragged row range [offsets[e], offsets[e+1]):
+ *   out[e, c, r] = sum_m  rsrc[rrow(m), r] * csrc[crow(m), c]
+ * rrow(m) = r_gather ? r_gather[m] : m (same for c). Rows of rsrc are r_ld elements apart, rows of
+ * csrc c_ld apart. out is (E_glu, C, R) contiguous; experts with no rows get zeros.
+ * down:    out = grad_down_proj (E,H,I): rsrc = inter (R=I), csrc = grad_eo (C=H).
+ * gate_up: out = grad_gate_up_proj (E,2I,H): rsrc = hidden gathered by sorted_token (R=H),
+ *          csrc = ggu (C=2I).
+ * Replaces `_grouped_wgrad` (kernels/sm75/moe.py:507-532,556-561) and the per-expert
+ * `ge.t() @ it`, `grad_gate_up.t() @ x_s[s:en]` (:808,821). */
+int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
+                      const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R, int64_t C,
+                      const int32_t* offsets, int E_glu, void* out, void* stream);
+
+/* Un-permute backward: grad_x[t] = sum_j contribution(t,j) in slot order, fp32 accumulation;
+ * contribution = grad_xs[flat_to_sorted[t*k+j]] (GLU), w * grad_out[t] (Identity), 0 (Zero).
+ * Replaces grad_x.index_add_(0, st, grad_x_s) (kernels/sm75/moe.py:614-615,822) and the Identity
+ * backward (:796-799). */
+int moe_unpermute_bwd(int dtype, const void* grad_xs, const void* grad_out, int64_t grad_out_ld,
+                      const void* top_k_weights, const int64_t* top_k_indices,
+                      const int32_t* act_codes, int n_experts, int E_glu,
+                      const int32_t* flat_to_sorted,
+                      int64_t n_tokens, int top_k, int64_t H, void* grad_x_out, void* stream);
+
+/* Row-wise PolyGLU activation (BatchedGLU, kernels/sm75/moe.py:450-474): for every row m with
+ * code c = row_act[m]: out[m] = act_c(gate) * up, codes 0,1,2,5,6,7 (kernels/sm75/moe.py:163-184).
+ * gate_up rows are gu_ld elements apart, out rows out_ld apart. alpha/gamma: per-row fp32 SiTU
+ * scalars with stride ap_stride (0 = one value for every row); NULL means 1.0. */
+int moe_glu_fwd(int dtype, const void* gate_up, int64_t gu_ld, const int32_t* row_act,
+                const float* alpha, const float* gamma, int ap_stride, int64_t n_rows, int64_t I,
+                void* out, int64_t out_ld, void* stream);
+
+/* Row-wise PolyGLU backward (kernels/sm75/moe.py:187-232): ggu = [d gate, d up]; when da/dg are
+ * non-NULL, the per-row SiTU parameter gradients (0 for rows whose code is not 5). grad_out
+ * elements are (go_row_stride, go_col_stride) apart, so broadcast grads need no copy. */
+int moe_glu_bwd(int dtype, const void* grad_out, int64_t go_row_stride, int64_t go_col_stride,
+                const void* gate_up, int64_t gu_ld, const int32_t* row_act, const float* alpha,
+                const float* gamma, int ap_stride, int64_t n_rows, int64_t I, void* ggu_out,
+                int64_t ggu_ld, float* da_out, float* dg_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_GFX950_H */

@@ -1,0 +1,138 @@
+"""CPU checks of the C-ABI library and the host-side Python layer (no GPU compute)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from kernels import _lib
+import kernels
+import importlib
+moe_mod = importlib.import_module("kernels.gfx950.moe")
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moe_gfx950.h")
+
+
+def _header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    h = _lib.lib()
+    declared = _header_symbols()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(h, name), name
+    assert set(declared) == set(_lib.declared_symbols())
+
+
+def test_version_and_tile_rows():
+    assert _lib.lib().moe_version().startswith(b"moe_gfx950")
+    assert _lib.lib().moe_tile_rows() == 128
+
+
+def test_workspace_size():
+    ws = _lib.lib().moe_get_workspace_size
+    assert ws(16384, 8, 64) >= (131072 // 4096) * 64 * 4
+    assert ws(0, 2, 8) > 0
+    assert ws(-1, 2, 8) == 0
+
+
+# Argument validation happens on the host before any HIP call, so these run without a GPU.
+def test_dispatch_rejects_bad_arguments():
+    h = _lib.lib()
+    assert h.moe_dispatch(None, 4, 2, 0, None, None, None, None, None, None, None, None, 0, None) == 1
+    assert h.moe_dispatch(None, 4, 2, 2000, None, None, None, None, None, None, None, None, 0, None) == 1
+    fake = ctypes.c_void_p(16)
+    assert h.moe_dispatch(fake, 4, 2, 8, fake, fake, fake, fake, fake, fake, fake, None, 0, None) == 6
+
+
+def test_gemm_entry_points_reject_bad_arguments():
+    h = _lib.lib()
+    fake = 256
+    # dtype
+    assert h.moe_grouped_down_fwd(7, fake, fake, 4, 64, 64, fake, None, 10, fake, None) == 4
+    # H not a multiple of 8
+    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 60, 64, fake, None, 10, fake, None) == 2
+    # misaligned pointer
+    assert h.moe_grouped_down_fwd(2, fake + 2, fake, 4, 64, 64, fake, None, 10, fake, None) == 2
+    # no experts
+    assert h.moe_grouped_down_fwd(2, fake, fake, 0, 64, 64, fake, None, 10, fake, None) == 1
+    # zero rows is a no-op success
+    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 64, 64, fake, None, 0, fake, None) == 0
+    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, 4, fake, None) == 2
+    assert h.moe_combine_fwd(2, fake, fake, fake, fake, fake, 4, 5, fake, 10, 2, 64, fake, None) == 1
+    assert h.moe_glu_fwd(2, fake, 10, fake, fake, None, 1, 4, 8, fake, 8, None) == 1
+
+
+def test_call_maps_status_to_exceptions():
+    with pytest.raises(TypeError):
+        _lib.call("moe_grouped_down_fwd", 9, 16, 16, 4, 64, 64, 16, None, 10, 16, None)
+    with pytest.raises(ValueError):
+        _lib.call("moe_grouped_down_fwd", 2, 18, 16, 4, 64, 64, 16, None, 10, 16, None)
+
+
+def test_host_tensors_fail_loudly():
+    x = torch.randn(8, 16)
+    idx = torch.zeros(8, 2, dtype=torch.long)
+    w = torch.ones(8, 2) / 2
+    gu = torch.randn(2, 16, 16)
+    dw = torch.randn(2, 16, 8)
+    codes = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="device"):
+        kernels.moe(x, idx, w, gu, dw, codes)
+
+
+def test_code_order_validation():
+    with pytest.raises(ValueError):
+        moe_mod._check_codes((0, 3, 0), 3)
+    with pytest.raises(ValueError):
+        moe_mod._check_codes((0, 0, 1), 2)
+    moe_mod._check_codes((0, 1, 2, 5, 6, 7, 3, 4), 6)
+
+
+def test_grouped_rejects_situ_like_reference():
+    codes = torch.tensor([0, 5], dtype=torch.int32)
+    with pytest.raises(ValueError, match="code 5"):
+        kernels.moe_grouped(torch.zeros(1, 8), torch.zeros(1, 1, dtype=torch.long),
+                            torch.ones(1, 1), torch.zeros(2, 16, 8), torch.zeros(2, 8, 8), codes)
+    with pytest.raises(ValueError, match="code 5"):
+        kernels.moe_grouped_cublas_polyglu(torch.zeros(1, 8), torch.zeros(1, 1, dtype=torch.long),
+                                           torch.ones(1, 1), torch.zeros(2, 16, 8),
+                                           torch.zeros(2, 8, 8), codes)
+
+
+def test_batched_glu_half_specified_params():
+    with pytest.raises(ValueError):
+        kernels.BatchedGLU.apply(torch.zeros(2, 8), torch.zeros(2, dtype=torch.int32),
+                                 torch.ones(2), None)
+
+
+def test_import_aliases():
+    from kernels.sm75 import moe as m75
+    from kernels.sm120 import moe as m120
+    from kernels.sm120.moe_grouped import grouped_supported, prefer_grouped
+    from kernels.sm75.moe import moe_eager
+    assert callable(m75) and callable(m120) and callable(moe_eager)
+    assert not grouped_supported(torch.zeros(2, 8), torch.zeros(1, 16, 8), torch.zeros(1, 8, 8))
+    assert prefer_grouped(torch.zeros(4, 2), torch.zeros(8, 2, 2))
+
+
+def test_moe_eager_matches_oracle_on_cpu():
+    # the API's eager reference (pure PyTorch) agrees with the oracle restatement
+    from oracle import moe_oracle as orc
+    g = torch.Generator().manual_seed(0)
+    codes = [0, 1, 2, 5, 3, 4]
+    x = torch.randn(40, 16, generator=g)
+    gu = torch.randn(4, 32, 16, generator=g) * 0.3
+    dw = torch.randn(4, 16, 16, generator=g) * 0.3
+    idx = torch.rand(40, 6, generator=g).topk(2, -1).indices
+    wt = torch.rand(40, 2, generator=g)
+    ap = torch.rand(6, 2, generator=g) + 0.5
+    a = kernels.moe_eager(x, idx, wt, gu, dw, torch.tensor(codes, dtype=torch.int32), ap)
+    b = orc.moe_forward(x, idx, wt, gu, dw, codes, ap)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)

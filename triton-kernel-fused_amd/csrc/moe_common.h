@@ -1,0 +1,80 @@
+// Shared device helpers for the gfx950 MoE kernels: element types, 16-byte vector access,
+// MFMA wrappers and the dtype / status codes of the C ABI (declared in include/moe_gfx950.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_gfx950.h"
+
+namespace moe {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
+
+// Round a float through T and back (the value a stored-then-reloaded T would have).
+template <typename T> __device__ __forceinline__ float round_through(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+// MFMA traits per element type. Each lane holds one 16-byte chunk of K per "slab": the two lane
+// halves (lanes 0-31 and 32-63) hold consecutive 16-byte chunks, so one slab spans 32 bytes of K.
+// Operand P feeds the MFMA A side (rows of the 32x32 output), operand Q the B side (columns).
+template <typename T> struct Mfma;
+
+template <> struct Mfma<bf16> {
+  static constexpr int VEC = 8;  // elements per 16 bytes
+  __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<f16> {
+  static constexpr int VEC = 8;
+  __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma<float> {
+  static constexpr int VEC = 4;
+  // v_mfma_f32_32x32x2f32 consumes one fp32 per lane and K=2 per instruction (one value per lane
+  // half), so a 16-byte chunk (4 consecutive K values per lane) is four instructions.
+  __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
+    // Bit-cast whole vectors: this compiler folds a bit-cast of a single vector element to
+    // element 0, so per-element casts (vec[j]) must not be used.
+    const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j], bf[j], c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ i32x4 ldg16(const void* p) { return *(const i32x4*)p; }
+__device__ __forceinline__ void stg16(void* p, i32x4 v) { *(i32x4*)p = v; }
+__device__ __forceinline__ i32x4 zero4() { return i32x4{0, 0, 0, 0}; }
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// 64-bit wave ballot.
+__device__ __forceinline__ unsigned long long ballot64(bool p) { return __ballot(p); }
+
+}  // namespace moe

@@ -1,0 +1,189 @@
+// Token dispatch for the grouped expert GEMMs: per-expert histogram, prefix scan and a stable
+// permutation of the N*k routed rows ordered by (expert id, flat index t*k+j).
+//
+// The reference sorts the flattened expert ids with torch's (unstable) sort and then syncs the
+// host with bincount(...).tolist() (/root/reference/kernels/sm75/moe.py:564-572); its grouped
+// schedule is a host loop (:535-543). Here everything stays on the device:
+//   pass 1 (hist):    each chunk of DISPATCH_CHUNK flat rows counts its experts in LDS;
+//   pass 2 (scan):    one workgroup turns the chunk histograms into per-chunk base offsets,
+//                     per-expert counts, offsets and token-tile offsets;
+//   pass 3 (scatter): each chunk re-reads its rows and ranks them stably. Within a wave the rank
+//                     of a row among equal experts comes from a ballot match (one ballot per id
+//                     bit) and a popcount; waves of one step are ordered through LDS counters.
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int DISPATCH_THREADS = 256;
+constexpr int DISPATCH_CHUNK = 4096;  // flat rows per chunk (16 steps of 256)
+constexpr int MAX_EXPERTS = 1024;
+constexpr int TILE_ROWS = 128;        // token-tile height of the grouped GEMMs
+
+__device__ __forceinline__ int load_expert(const int64_t* idx, int64_t f, int E, bool& valid) {
+  int64_t v = idx[f];
+  valid = (v >= 0) && (v < E);
+  return valid ? (int)v : E;
+}
+
+__global__ void __launch_bounds__(DISPATCH_THREADS)
+dispatch_hist_kernel(const int64_t* __restrict__ idx, int64_t M, int E, int32_t* __restrict__ hist,
+                     int32_t* __restrict__ status) {
+  __shared__ int cnt[MAX_EXPERTS + 1];
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e <= E; e += DISPATCH_THREADS) cnt[e] = 0;
+  __syncthreads();
+  const int64_t f0 = (int64_t)b * DISPATCH_CHUNK;
+  int bad = 0;
+  for (int i = threadIdx.x; i < DISPATCH_CHUNK; i += DISPATCH_THREADS) {
+    int64_t f = f0 + i;
+    if (f < M) {
+      bool valid;
+      int e = load_expert(idx, f, E, valid);
+      atomicAdd(&cnt[e], 1);
+      bad += valid ? 0 : 1;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += DISPATCH_THREADS) hist[(int64_t)b * E + e] = cnt[e];
+  if (bad) atomicAdd(status, bad);
+}
+
+// One workgroup. hist (nchunks, E) is rewritten in place into exclusive per-chunk bases.
+__global__ void __launch_bounds__(1024)
+dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E, int32_t* __restrict__ counts,
+                     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets) {
+  __shared__ int s_cnt[MAX_EXPERTS];
+  __shared__ int s_tiles[MAX_EXPERTS];
+  const int e = threadIdx.x;
+  if (e < E) {
+    int run = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      int v = hist[(int64_t)c * E + e];
+      hist[(int64_t)c * E + e] = run;
+      run += v;
+    }
+    counts[e] = run;
+    s_cnt[e] = run;
+    s_tiles[e] = (run + TILE_ROWS - 1) / TILE_ROWS;
+  }
+  __syncthreads();
+  // E <= 1024: a serial scan by one thread is a few microseconds at most and keeps this exact.
+  if (threadIdx.x == 0) {
+    int o = 0, t = 0;
+    for (int i = 0; i < E; ++i) {
+      offsets[i] = o;
+      tile_offsets[i] = t;
+      o += s_cnt[i];
+      t += s_tiles[i];
+    }
+    offsets[E] = o;
+    tile_offsets[E] = t;
+  }
+}
+
+__global__ void __launch_bounds__(DISPATCH_THREADS)
+dispatch_scatter_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int E,
+                        const int32_t* __restrict__ chunk_base, const int32_t* __restrict__ offsets,
+                        int32_t* __restrict__ sorted_token, int32_t* __restrict__ sorted_flat,
+                        int32_t* __restrict__ flat_to_sorted) {
+  constexpr int NW = DISPATCH_THREADS / 64;
+  __shared__ int run[MAX_EXPERTS + 1];        // rows of each expert already placed by this chunk
+  __shared__ int wcnt[NW][MAX_EXPERTS + 1];   // rows of each expert in each wave of this step
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e <= E; e += DISPATCH_THREADS) {
+    run[e] = (e < E) ? offsets[e] + chunk_base[(int64_t)b * E + e] : 0;
+  }
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E = invalid bucket)
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  const int64_t f0 = (int64_t)b * DISPATCH_CHUNK;
+  for (int s = 0; s < DISPATCH_CHUNK; s += DISPATCH_THREADS) {
+    for (int i = threadIdx.x; i < NW * (E + 1); i += DISPATCH_THREADS) wcnt[i / (E + 1)][i % (E + 1)] = 0;
+    __syncthreads();
+    const int64_t f = f0 + s + threadIdx.x;
+    const bool live = f < M;
+    bool valid = false;
+    int e = live ? load_expert(idx, f, E, valid) : E;
+    // Lanes holding the same id: intersect the ballots of every id bit.
+    unsigned long long match = ballot64(live);
+#pragma unroll 1
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (e >> bit) & 1;
+      const unsigned long long bl = ballot64(live && on);
+      match &= on ? bl : ~bl;
+    }
+    if (!live) match = 0;
+    const int rank = __popcll(match & lt_mask);
+    if (live && rank == 0) wcnt[w][e] = __popcll(match);
+    __syncthreads();
+    if (live) {
+      if (valid) {
+        int pos = run[e] + rank;
+        for (int ww = 0; ww < w; ++ww) pos += wcnt[ww][e];
+        sorted_token[pos] = (int32_t)(f / top_k);
+        sorted_flat[pos] = (int32_t)f;
+        flat_to_sorted[f] = pos;
+      } else {
+        flat_to_sorted[f] = -1;
+      }
+    }
+    __syncthreads();
+    for (int ee = threadIdx.x; ee < E; ee += DISPATCH_THREADS) {
+      int add = 0;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) add += wcnt[ww][ee];
+      run[ee] += add;
+    }
+    // The next step's clear of wcnt is ordered after these reads by its own barrier below.
+    __syncthreads();
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+static int64_t n_chunks(int64_t M) { return (M + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK; }
+
+extern "C" int moe_tile_rows(void) { return TILE_ROWS; }
+
+extern "C" size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_experts) {
+  if (n_tokens < 0 || top_k <= 0 || n_experts <= 0) return 0;
+  int64_t M = n_tokens * top_k;
+  int64_t nc = n_chunks(M);
+  if (nc < 1) nc = 1;
+  size_t bytes = (size_t)nc * (size_t)n_experts * sizeof(int32_t);
+  return (bytes + 255) & ~(size_t)255;
+}
+
+extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
+                            int n_experts, int32_t* counts, int32_t* offsets,
+                            int32_t* tile_offsets, int32_t* sorted_token, int32_t* sorted_flat,
+                            int32_t* flat_to_sorted, int32_t* status, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (n_tokens < 0 || top_k <= 0 || n_experts <= 0 || n_experts > MAX_EXPERTS) return MOE_ERR_SHAPE;
+  const int64_t M = n_tokens * top_k;
+  if (M >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  if (!counts || !offsets || !tile_offsets || !status) return MOE_ERR_SHAPE;
+  if (M > 0 && (!top_k_indices || !sorted_token || !sorted_flat || !flat_to_sorted))
+    return MOE_ERR_SHAPE;
+  if (!workspace || workspace_bytes < moe_get_workspace_size(n_tokens, top_k, n_experts))
+    return MOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* hist = (int32_t*)workspace;
+  const int nc = (int)n_chunks(M);
+  if (nc > 0) {
+    hipLaunchKernelGGL(dispatch_hist_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s, top_k_indices,
+                       M, n_experts, hist, status);
+  }
+  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, nc, n_experts, counts,
+                     offsets, tile_offsets);
+  if (nc > 0) {
+    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s,
+                       top_k_indices, M, top_k, n_experts, hist, offsets, sorted_token,
+                       sorted_flat, flat_to_sorted);
+  }
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}

@@ -1,0 +1,721 @@
+// Grouped expert GEMMs for gfx950: forward gate/up (+GLU epilogue), forward down, backward dX of
+// both projections (+GLU-backward epilogue on the down one) and the ragged weight gradients.
+//
+// One MFMA mainloop serves all of them. The output tile is BR "P rows" x BC "Q columns"; P feeds
+// the MFMA A side and is always the operand whose index is contiguous in the output, so each lane
+// ends up owning four consecutive output elements (one 8-byte bf16 store). Both operands are
+// staged through LDS as [row][128 bytes of K] with a 16-byte pad per row (conflict-free 16-byte
+// reads for 16 consecutive rows), double-buffered with one barrier per K step. Operands that are
+// K-contiguous in HBM are copied as 16-byte chunks; operands that are row-contiguous (weights
+// read transposed, and every wgrad operand) are loaded as VECxVEC blocks and transposed in
+// registers before the LDS store, so the MFMA always reads 16 contiguous K bytes per lane.
+//
+// Token GEMMs walk variable-size expert groups: every workgroup rebuilds the per-expert tile
+// prefix from the dispatch offsets in LDS (a block scan), finds its expert by binary search and
+// exits if its tile is past the end, so the grid is a host-side upper bound and nothing syncs.
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int BK_BYTES = 128;
+constexpr int LDS_ROW = BK_BYTES + 16;
+constexpr int MAX_GLU_EXPERTS = 1024;
+
+enum EpiMode { EPI_STORE = 0, EPI_GLU_FWD = 1, EPI_GLU_BWD = 2 };
+
+template <typename T_, int BR_, int BC_, int WR_, int WC_>
+struct Cfg {
+  typedef T_ T;
+  static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
+  static constexpr int NT = WR * WC * 64;
+  static constexpr int VEC = 16 / (int)sizeof(T);
+  static constexpr int BK = BK_BYTES / (int)sizeof(T);
+  static constexpr int WTR = BR / WR;
+  static constexpr int WTC = BC / WC;
+  static constexpr int TI = WTR / 32;
+  static constexpr int TJ = WTC / 32;
+  static constexpr int SLABS = BK_BYTES / 32;
+  static constexpr int LDS_P = BR * LDS_ROW;
+  static constexpr int LDS_Q = BC * LDS_ROW;
+  static constexpr int STAGE = LDS_P + LDS_Q;
+  static constexpr int LDS_BYTES = 2 * STAGE;
+  static_assert(WTR % 32 == 0 && WTC % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
+};
+
+// ---------------------------------------------------------------------------------------------
+// Loaders. fetch() issues the global loads of one K step into registers, store() writes them to
+// one LDS stage. Rows outside the valid range and K beyond the end load zeros.
+
+// K-contiguous rows: chunk c = tid + i*NT covers tile row c/8, 16-byte K chunk c%8.
+template <typename T, int ROWS, int NT>
+struct KcLoader {
+  static constexpr int VEC = 16 / (int)sizeof(T);
+  static constexpr int CPR = BK_BYTES / 16;
+  static constexpr int CPT = ROWS * CPR / NT;
+  static_assert((ROWS * CPR) % NT == 0 && NT % CPR == 0, "chunk split");
+  const char* row[CPT];
+  i32x4 reg[CPT];
+  int kc;
+  int K;
+
+  __device__ __forceinline__ static int row_of(int i) {
+    return (int)(threadIdx.x / CPR) + i * (NT / CPR);
+  }
+  __device__ __forceinline__ void fetch(int k0) {
+    const int k = k0 + kc * VEC;
+    const bool kin = k < K;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+      reg[i] = (row[i] != nullptr && kin) ? ldg16(row[i] + (size_t)k * sizeof(T)) : zero4();
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) *(i32x4*)(lds + row_of(i) * LDS_ROW + kc * 16) = reg[i];
+  }
+};
+
+// in[j] = VEC values (index r) of K row j  ->  out[r] = the VEC K values of column r.
+__device__ __forceinline__ void transpose_unit(const i32x4 (&in)[8], i32x4 (&out)[8]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const unsigned sel = (r & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      out[r][w] = (int)__builtin_amdgcn_perm((unsigned)in[2 * w + 1][r >> 1],
+                                             (unsigned)in[2 * w][r >> 1], sel);
+  }
+}
+__device__ __forceinline__ void transpose_unit(const i32x4 (&in)[4], i32x4 (&out)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[r][j] = in[j][r];
+}
+
+// Row-contiguous operand: element (r, k) at src + row(k)*ld + r with row(k) = gather ? gather[k]
+// : k. Unit u = tid + i*NT covers VEC rows r (chunk rc = u % RCH) x VEC K values (kc = u / RCH);
+// rc runs fastest so a wave's loads of one K row are contiguous.
+template <typename T, int ROWS, int NT>
+struct RcLoader {
+  static constexpr int VEC = 16 / (int)sizeof(T);
+  static constexpr int RCH = ROWS / VEC;
+  static constexpr int KCH = BK_BYTES / 16;
+  static constexpr int UNITS = RCH * KCH;
+  static constexpr int UPT = (UNITS + NT - 1) / NT;
+  const char* src;  // column r0 of row 0
+  size_t ld;        // bytes between rows
+  const int32_t* gather;
+  int kend;    // K values >= kend load zeros
+  int rvalid;  // tile rows >= rvalid load zeros (a multiple of VEC)
+  i32x4 reg[UPT][VEC];
+
+  __device__ __forceinline__ void fetch(int k0) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = (int)threadIdx.x + i * NT;
+      if (UNITS % NT == 0 || u < UNITS) {
+        const int rc = u % RCH, kc = u / RCH;
+        const bool rin = rc * VEC < rvalid;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const int k = k0 + kc * VEC + j;
+          if (rin && k < kend) {
+            const int rowi = gather ? gather[k] : k;
+            reg[i][j] = ldg16(src + (size_t)rowi * ld + (size_t)rc * 16);
+          } else {
+            reg[i][j] = zero4();
+          }
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int u = (int)threadIdx.x + i * NT;
+      if (UNITS % NT == 0 || u < UNITS) {
+        const int rc = u % RCH, kc = u / RCH;
+        i32x4 t[VEC];
+        transpose_unit(reg[i], t);
+#pragma unroll
+        for (int r = 0; r < VEC; ++r) *(i32x4*)(lds + (rc * VEC + r) * LDS_ROW + kc * 16) = t[r];
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Mainloop: acc[ti][tj] += P_tile(rows) . Q_tile(cols) over K in [k_begin, k_end).
+template <class C, class LP, class LQ>
+__device__ __forceinline__ void mainloop(f32x16 (&acc)[C::TI][C::TJ], LP& lp, LQ& lq, int k_begin,
+                                         int k_end, char* smem) {
+  const int nk = (k_end - k_begin + C::BK - 1) / C::BK;
+  if (nk <= 0) return;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int pa_off = (wr * C::WTR + (lane & 31)) * LDS_ROW + (lane >> 5) * 16;
+  const int qb_off = C::LDS_P + (wc * C::WTC + (lane & 31)) * LDS_ROW + (lane >> 5) * 16;
+
+  lp.fetch(k_begin);
+  lq.fetch(k_begin);
+  lp.store(smem);
+  lq.store(smem + C::LDS_P);
+  __syncthreads();
+  for (int it = 0; it < nk; ++it) {
+    char* cur = smem + (it & 1) * C::STAGE;
+    const bool more = it + 1 < nk;
+    if (more) {
+      lp.fetch(k_begin + (it + 1) * C::BK);
+      lq.fetch(k_begin + (it + 1) * C::BK);
+    }
+#pragma unroll
+    for (int s = 0; s < C::SLABS; ++s) {
+      i32x4 a[C::TI], b[C::TJ];
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+        a[ti] = *(const i32x4*)(cur + pa_off + ti * 32 * LDS_ROW + s * 32);
+#pragma unroll
+      for (int tj = 0; tj < C::TJ; ++tj)
+        b[tj] = *(const i32x4*)(cur + qb_off + tj * 32 * LDS_ROW + s * 32);
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < C::TJ; ++tj) Mfma<typename C::T>::step(acc[ti][tj], a[ti], b[tj]);
+    }
+    if (more) {
+      char* nxt = smem + ((it + 1) & 1) * C::STAGE;
+      lp.store(nxt);
+      lq.store(nxt + C::LDS_P);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Output helpers: four consecutive elements of one row.
+template <typename T> struct Store4;
+template <> struct Store4<bf16> {
+  __device__ __forceinline__ static void st(bf16* p, float a, float b, float c, float d) {
+    bf16x2 lo = {(bf16)a, (bf16)b}, hi = {(bf16)c, (bf16)d};
+    uint2 v = {__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi)};
+    *(uint2*)p = v;
+  }
+  __device__ __forceinline__ static void ld(const bf16* p, float (&v)[4]) {
+    uint2 u = *(const uint2*)p;
+    bf16x2 lo = __builtin_bit_cast(bf16x2, u.x), hi = __builtin_bit_cast(bf16x2, u.y);
+    v[0] = (float)lo[0]; v[1] = (float)lo[1]; v[2] = (float)hi[0]; v[3] = (float)hi[1];
+  }
+};
+template <> struct Store4<f16> {
+  __device__ __forceinline__ static void st(f16* p, float a, float b, float c, float d) {
+    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 h4;
+    h4 v = {(f16)a, (f16)b, (f16)c, (f16)d};
+    *(h4*)p = v;
+  }
+  __device__ __forceinline__ static void ld(const f16* p, float (&v)[4]) {
+    typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 h4;
+    h4 u = *(const h4*)p;
+    v[0] = (float)u[0]; v[1] = (float)u[1]; v[2] = (float)u[2]; v[3] = (float)u[3];
+  }
+};
+template <> struct Store4<float> {
+  __device__ __forceinline__ static void st(float* p, float a, float b, float c, float d) {
+    *(f32x4*)p = f32x4{a, b, c, d};
+  }
+  __device__ __forceinline__ static void ld(const float* p, float (&v)[4]) {
+    f32x4 u = *(const f32x4*)p;
+    v[0] = u[0]; v[1] = u[1]; v[2] = u[2]; v[3] = u[3];
+  }
+};
+
+// GLU activation and its derivative for the codes the GEMM epilogues fuse (0 = SiLU, 1 = ReLU^2),
+// kernels/sm75/moe.py:176-183 (forward) and :206-225 (backward).
+__device__ __forceinline__ float glu_act(int code, float g) {
+  if (code == 1) { float r = fmaxf(g, 0.f); return r * r; }
+  return silu(g);
+}
+__device__ __forceinline__ float glu_dact(int code, float g) {
+  if (code == 1) return 2.f * fmaxf(g, 0.f);
+  const float s = sigmoid(g);
+  return s * (1.f + g * (1.f - s));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Token-grouped GEMM: for each expert e < E_glu and each tile of its sorted rows,
+//   acc[r, m] = sum_k P_e[r, k] * Q[qrow(m), k].
+struct TokenArgs {
+  const void* P;      // expert weights base
+  long long p_e;      // elements between experts
+  long long p_ld;     // elements between rows (P_KC) or between K rows (P_RC)
+  int R;              // P rows per expert (output row dim); EPI_GLU_FWD: 2*I
+  int K;
+  const void* Q;      // token-side operand rows (K-contiguous)
+  long long q_ld;     // elements between rows
+  const int32_t* q_gather;  // sorted row -> Q row (sorted_token), or null for identity
+  const int32_t* offsets;   // E_glu + 1 sorted-row offsets
+  int E_glu;
+  int n_rtiles;
+  const int32_t* act_codes;
+  int I;              // intermediate size (GLU epilogues)
+  void* out;          // EPI_STORE: (M, R); EPI_GLU_FWD: gate_up (M, 2I); EPI_GLU_BWD: ggu (M, 2I)
+  long long out_ld;
+  void* out2;         // EPI_GLU_FWD: inter (M, I); EPI_GLU_BWD: grad_inter (M, I)
+  const void* aux;    // EPI_GLU_BWD: gate_up (M, 2I)
+};
+
+// Block-wide exclusive scan of the per-expert tile counts into s_pref[0..E]; returns the total.
+template <int NT>
+__device__ __forceinline__ void tile_prefix(const int32_t* offsets, int E, int BC, int* s_pref,
+                                            int* s_wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int per = (E + NT - 1) / NT;
+  const int e0 = tid * per;
+  int local = 0;
+  for (int j = 0; j < per; ++j) {
+    const int e = e0 + j;
+    if (e < E) local += (offsets[e + 1] - offsets[e] + BC - 1) / BC;
+  }
+  int incl = local;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int v = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += v;
+  }
+  if (lane == 63) s_wsum[wid] = incl;
+  __syncthreads();
+  int run = incl - local;
+  for (int w = 0; w < wid; ++w) run += s_wsum[w];
+  for (int j = 0; j < per; ++j) {
+    const int e = e0 + j;
+    if (e < E) {
+      s_pref[e] = run;
+      run += (offsets[e + 1] - offsets[e] + BC - 1) / BC;
+    }
+  }
+  if (tid == NT - 1) s_pref[E] = run;
+  __syncthreads();
+}
+
+template <class C, int EPI, bool P_RC>
+__global__ void __launch_bounds__(C::NT)
+token_gemm_kernel(TokenArgs a) {
+  typedef typename C::T T;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
+  __shared__ int s_wsum[C::NT / 64];
+
+  tile_prefix<C::NT>(a.offsets, a.E_glu, C::BC, s_pref, s_wsum);
+  const int mt = (int)(blockIdx.x / a.n_rtiles);
+  const int rt = (int)(blockIdx.x % a.n_rtiles);
+  if (mt >= s_pref[a.E_glu]) return;
+  int lo = 0, hi = a.E_glu - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
+  }
+  const int e = lo;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * C::BC;
+  const int m_end = a.offsets[e + 1];
+
+  const int tid = threadIdx.x;
+  const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
+
+  // Q: sorted token rows m0 .. m0+BC (K-contiguous, optionally gathered).
+  KcLoader<T, C::BC, C::NT> lq;
+  lq.kc = tid % lq.CPR;
+  lq.K = a.K;
+#pragma unroll
+  for (int i = 0; i < lq.CPT; ++i) {
+    const int m = m0 + lq.row_of(i);
+    if (m < m_end) {
+      const int qr = a.q_gather ? a.q_gather[m] : m;
+      lq.row[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
+    } else {
+      lq.row[i] = nullptr;
+    }
+  }
+
+  f32x16 acc[C::TI][C::TJ];
+#pragma unroll
+  for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < C::TJ; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+
+  if constexpr (P_RC) {
+    // P[r, k] at Pe + k*p_ld + r (a weight read transposed).
+    RcLoader<T, C::BR, C::NT> lp;
+    const int r0 = rt * C::BR;
+    lp.src = (const char*)(Pe + r0);
+    lp.ld = (size_t)a.p_ld * sizeof(T);
+    lp.gather = nullptr;
+    lp.kend = a.K;
+    lp.rvalid = a.R - r0;
+    mainloop<C>(acc, lp, lq, 0, a.K, smem);
+  } else {
+    KcLoader<T, C::BR, C::NT> lp;
+    lp.kc = tid % lp.CPR;
+    lp.K = a.K;
+#pragma unroll
+    for (int i = 0; i < lp.CPT; ++i) {
+      const int rr = lp.row_of(i);
+      int prow;
+      bool ok;
+      if (EPI == EPI_GLU_FWD) {
+        // Interleave gate and up: in each wave's WTR rows the first half are gate channels and
+        // the second half the same up channels, so the epilogue pairs them in registers.
+        const int wr = rr / C::WTR, w = rr % C::WTR;
+        const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + (w % (C::WTR / 2));
+        ok = ch < a.I;
+        prow = (w >= C::WTR / 2 ? a.I : 0) + ch;
+      } else {
+        prow = rt * C::BR + rr;
+        ok = prow < a.R;
+      }
+      lp.row[i] = ok ? (const char*)(Pe + (size_t)prow * a.p_ld) : nullptr;
+    }
+    mainloop<C>(acc, lp, lq, 0, a.K, smem);
+  }
+
+  // Epilogue.
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int h = lane >> 5;
+  // act_codes is NULL when the epilogue only writes raw GEMM results (grad_inter mode).
+  const int code = (EPI == EPI_STORE || a.act_codes == nullptr) ? 0 : a.act_codes[e];
+#pragma unroll
+  for (int tj = 0; tj < C::TJ; ++tj) {
+    const int m = m0 + wc * C::WTC + tj * 32 + (lane & 31);
+    if (m >= m_end) continue;
+    if constexpr (EPI == EPI_STORE) {
+      T* o = (T*)a.out + (size_t)m * a.out_ld;
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+          if (r < a.R)
+            Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1],
+                          acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3]);
+        }
+    } else if constexpr (EPI == EPI_GLU_FWD) {
+      T* gu = (T*)a.out + (size_t)m * 2 * a.I;
+      T* it = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
+#pragma unroll
+      for (int ti = 0; ti < C::TI / 2; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + ti * 32 + 8 * g + 4 * h;
+          if (ch >= a.I) continue;
+          float gv[4], uv[4], iv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            gv[j] = round_through<T>(acc[ti][tj][4 * g + j]);
+            uv[j] = round_through<T>(acc[ti + C::TI / 2][tj][4 * g + j]);
+            iv[j] = glu_act(code, gv[j]) * uv[j];
+          }
+          Store4<T>::st(gu + ch, gv[0], gv[1], gv[2], gv[3]);
+          Store4<T>::st(gu + a.I + ch, uv[0], uv[1], uv[2], uv[3]);
+          if (it) Store4<T>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
+        }
+    } else {  // EPI_GLU_BWD: acc = grad_inter[m, i]
+      const T* gu = (const T*)a.aux + (size_t)m * 2 * a.I;
+      T* ggu = a.out ? (T*)a.out + (size_t)m * 2 * a.I : nullptr;
+      T* gi = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i0 = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+          if (i0 >= a.I) continue;
+          float go[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) go[j] = round_through<T>(acc[ti][tj][4 * g + j]);
+          if (gi) Store4<T>::st(gi + i0, go[0], go[1], go[2], go[3]);
+          if (ggu) {
+            float gv[4], uv[4], dg[4], du[4];
+            Store4<T>::ld(gu + i0, gv);
+            Store4<T>::ld(gu + a.I + i0, uv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dg[j] = go[j] * uv[j] * glu_dact(code, gv[j]);
+              du[j] = go[j] * glu_act(code, gv[j]);
+            }
+            Store4<T>::st(ggu + i0, dg[0], dg[1], dg[2], dg[3]);
+            Store4<T>::st(ggu + a.I + i0, du[0], du[1], du[2], du[3]);
+          }
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Ragged weight gradient: out[e, c, r] = sum_{m in rows(e)} rsrc[rrow(m), r] * csrc[crow(m), c].
+struct WgradArgs {
+  const void* rsrc; long long r_ld; const int32_t* r_gather;
+  const void* csrc; long long c_ld; const int32_t* c_gather;
+  int R, C;
+  const int32_t* offsets;
+  int n_rtiles, n_ctiles;
+  void* out;
+};
+
+template <class C>
+__global__ void __launch_bounds__(C::NT)
+wgrad_kernel(WgradArgs a) {
+  typedef typename C::T T;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int per_e = a.n_rtiles * a.n_ctiles;
+  const int e = (int)(blockIdx.x / per_e);
+  const int rem = (int)(blockIdx.x % per_e);
+  const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
+  const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
+  const int r0 = rt * C::BR, c0 = ct * C::BC;
+
+  RcLoader<T, C::BR, C::NT> lp;
+  lp.src = (const char*)((const T*)a.rsrc + r0);
+  lp.ld = (size_t)a.r_ld * sizeof(T);
+  lp.gather = a.r_gather;
+  lp.kend = k1;
+  lp.rvalid = a.R - r0;
+  RcLoader<T, C::BC, C::NT> lq;
+  lq.src = (const char*)((const T*)a.csrc + c0);
+  lq.ld = (size_t)a.c_ld * sizeof(T);
+  lq.gather = a.c_gather;
+  lq.kend = k1;
+  lq.rvalid = a.C - c0;
+
+  f32x16 acc[C::TI][C::TJ];
+#pragma unroll
+  for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < C::TJ; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  mainloop<C>(acc, lp, lq, k0, k1, smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int h = lane >> 5;
+  T* outE = (T*)a.out + (size_t)e * a.C * a.R;
+#pragma unroll
+  for (int tj = 0; tj < C::TJ; ++tj) {
+    const int c = c0 + wc * C::WTC + tj * 32 + (lane & 31);
+    if (c >= a.C) continue;
+    T* o = outE + (size_t)c * a.R;
+#pragma unroll
+    for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = r0 + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+        if (r < a.R)
+          Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1], acc[ti][tj][4 * g + 2],
+                        acc[ti][tj][4 * g + 3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host-side launch helpers.
+
+template <typename T> using TokCfg = Cfg<T, 128, 128, 2, 2>;
+template <typename T> using WgCfg = Cfg<T, 128, 128, 2, 2>;
+
+template <class C, int EPI, bool P_RC>
+static int launch_token(const TokenArgs& a, int64_t n_rows, hipStream_t s) {
+  const int64_t max_mt = (n_rows + C::BC - 1) / C::BC + a.E_glu;
+  const int64_t grid = max_mt * a.n_rtiles;
+  if (grid <= 0 || n_rows == 0) return MOE_OK;
+  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  auto kern = token_gemm_kernel<C, EPI, P_RC>;
+  hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, s, a);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+template <class C>
+static int launch_wgrad(const WgradArgs& a, int E, hipStream_t s) {
+  const int64_t grid = (int64_t)E * a.n_rtiles * a.n_ctiles;
+  if (grid <= 0) return MOE_OK;
+  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  auto kern = wgrad_kernel<C>;
+  hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, s, a);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static int check_common(int dtype, int64_t H, int64_t I, int E_glu, int64_t n_rows) {
+  if (dtype != MOE_DT_F32 && dtype != MOE_DT_F16 && dtype != MOE_DT_BF16) return MOE_ERR_DTYPE;
+  if (H <= 0 || I <= 0 || E_glu <= 0 || E_glu > MAX_GLU_EXPERTS || n_rows < 0) return MOE_ERR_SHAPE;
+  if (H >= (1 << 30) || I >= (1 << 29) || n_rows >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
+  if (H % 8 != 0 || I % 8 != 0) return MOE_ERR_ALIGN;
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+#define MOE_DISPATCH_DTYPE(dtype, FN)                  \
+  switch (dtype) {                                     \
+    case MOE_DT_BF16: return FN<bf16>();               \
+    case MOE_DT_F16: return FN<f16>();                 \
+    case MOE_DT_F32: return FN<float>();               \
+    default: return MOE_ERR_DTYPE;                     \
+  }
+
+extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int64_t n_tokens,
+                                             int64_t H, const void* gate_up_proj, int E_glu,
+                                             int64_t I, const int32_t* act_codes,
+                                             const int32_t* offsets, const int32_t* tile_offsets,
+                                             const int32_t* sorted_token, int64_t n_rows,
+                                             void* gate_up_out, void* inter_out, void* stream) {
+  (void)tile_offsets;
+  int st = check_common(dtype, H, I, E_glu, n_rows);
+  if (st) return st;
+  if (n_rows == 0) return MOE_OK;
+  if (!hidden || !gate_up_proj || !offsets || !sorted_token || !gate_up_out || !act_codes)
+    return MOE_ERR_SHAPE;
+  if (!aligned16(hidden) || !aligned16(gate_up_proj) || !aligned16(gate_up_out) ||
+      (inter_out && !aligned16(inter_out)))
+    return MOE_ERR_ALIGN;
+  (void)n_tokens;
+  TokenArgs a = {};
+  a.P = gate_up_proj; a.p_e = 2 * I * H; a.p_ld = H; a.R = (int)(2 * I); a.K = (int)H;
+  a.Q = hidden; a.q_ld = H; a.q_gather = sorted_token;
+  a.offsets = offsets; a.E_glu = E_glu; a.act_codes = act_codes; a.I = (int)I;
+  a.out = gate_up_out; a.out_ld = 2 * I; a.out2 = inter_out;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&]<typename T>() {
+    using C = TokCfg<T>;
+    a.n_rtiles = (int)((I + C::BR / 2 - 1) / (C::BR / 2));
+    return launch_token<C, EPI_GLU_FWD, false>(a, n_rows, s);
+  };
+  switch (dtype) {
+    case MOE_DT_BF16: return go.template operator()<bf16>();
+    case MOE_DT_F16: return go.template operator()<f16>();
+    default: return go.template operator()<float>();
+  }
+}
+
+extern "C" int moe_grouped_down_fwd(int dtype, const void* inter, const void* down_proj, int E_glu,
+                                    int64_t H, int64_t I, const int32_t* offsets,
+                                    const int32_t* tile_offsets, int64_t n_rows, void* eo_out,
+                                    void* stream) {
+  (void)tile_offsets;
+  int st = check_common(dtype, H, I, E_glu, n_rows);
+  if (st) return st;
+  if (n_rows == 0) return MOE_OK;
+  if (!inter || !down_proj || !offsets || !eo_out) return MOE_ERR_SHAPE;
+  if (!aligned16(inter) || !aligned16(down_proj) || !aligned16(eo_out)) return MOE_ERR_ALIGN;
+  TokenArgs a = {};
+  a.P = down_proj; a.p_e = H * I; a.p_ld = I; a.R = (int)H; a.K = (int)I;
+  a.Q = inter; a.q_ld = I; a.q_gather = nullptr;
+  a.offsets = offsets; a.E_glu = E_glu; a.I = (int)I;
+  a.out = eo_out; a.out_ld = H;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&]<typename T>() {
+    using C = TokCfg<T>;
+    a.n_rtiles = (int)((H + C::BR - 1) / C::BR);
+    return launch_token<C, EPI_STORE, false>(a, n_rows, s);
+  };
+  switch (dtype) {
+    case MOE_DT_BF16: return go.template operator()<bf16>();
+    case MOE_DT_F16: return go.template operator()<f16>();
+    default: return go.template operator()<float>();
+  }
+}
+
+extern "C" int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo,
+                                              const void* down_proj, int E_glu, int64_t H,
+                                              int64_t I, const void* gate_up,
+                                              const int32_t* act_codes, const int32_t* offsets,
+                                              const int32_t* tile_offsets, int64_t n_rows,
+                                              void* ggu_out, void* grad_inter_out, void* stream) {
+  (void)tile_offsets;
+  int st = check_common(dtype, H, I, E_glu, n_rows);
+  if (st) return st;
+  if (n_rows == 0) return MOE_OK;
+  if (!grad_eo || !down_proj || !offsets || (!ggu_out && !grad_inter_out)) return MOE_ERR_SHAPE;
+  if (ggu_out && (!gate_up || !act_codes)) return MOE_ERR_SHAPE;
+  if (!aligned16(grad_eo) || !aligned16(down_proj) || (ggu_out && !aligned16(ggu_out)) ||
+      (gate_up && !aligned16(gate_up)) || (grad_inter_out && !aligned16(grad_inter_out)))
+    return MOE_ERR_ALIGN;
+  TokenArgs a = {};
+  // P[r = i, k = h] = down_proj[e, h, i]: row-contiguous, K rows I elements apart.
+  a.P = down_proj; a.p_e = H * I; a.p_ld = I; a.R = (int)I; a.K = (int)H;
+  a.Q = grad_eo; a.q_ld = H; a.q_gather = nullptr;
+  a.offsets = offsets; a.E_glu = E_glu; a.act_codes = act_codes; a.I = (int)I;
+  a.out = ggu_out; a.out2 = grad_inter_out; a.aux = gate_up;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&]<typename T>() {
+    using C = TokCfg<T>;
+    a.n_rtiles = (int)((I + C::BR - 1) / C::BR);
+    return launch_token<C, EPI_GLU_BWD, true>(a, n_rows, s);
+  };
+  switch (dtype) {
+    case MOE_DT_BF16: return go.template operator()<bf16>();
+    case MOE_DT_F16: return go.template operator()<f16>();
+    default: return go.template operator()<float>();
+  }
+}
+
+extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj,
+                                     int E_glu, int64_t H, int64_t I, const int32_t* offsets,
+                                     const int32_t* tile_offsets, int64_t n_rows,
+                                     void* grad_xs_out, void* stream) {
+  (void)tile_offsets;
+  int st = check_common(dtype, H, I, E_glu, n_rows);
+  if (st) return st;
+  if (n_rows == 0) return MOE_OK;
+  if (!ggu || !gate_up_proj || !offsets || !grad_xs_out) return MOE_ERR_SHAPE;
+  if (!aligned16(ggu) || !aligned16(gate_up_proj) || !aligned16(grad_xs_out)) return MOE_ERR_ALIGN;
+  TokenArgs a = {};
+  // P[r = h, k = n] = gate_up_proj[e, n, h]: row-contiguous, K rows H elements apart.
+  a.P = gate_up_proj; a.p_e = 2 * I * H; a.p_ld = H; a.R = (int)H; a.K = (int)(2 * I);
+  a.Q = ggu; a.q_ld = 2 * I; a.q_gather = nullptr;
+  a.offsets = offsets; a.E_glu = E_glu; a.I = (int)I;
+  a.out = grad_xs_out; a.out_ld = H;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&]<typename T>() {
+    using C = TokCfg<T>;
+    a.n_rtiles = (int)((H + C::BR - 1) / C::BR);
+    return launch_token<C, EPI_STORE, true>(a, n_rows, s);
+  };
+  switch (dtype) {
+    case MOE_DT_BF16: return go.template operator()<bf16>();
+    case MOE_DT_F16: return go.template operator()<f16>();
+    default: return go.template operator()<float>();
+  }
+}
+
+extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
+                                 const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R,
+                                 int64_t C, const int32_t* offsets, int E_glu, void* out,
+                                 void* stream) {
+  if (dtype != MOE_DT_F32 && dtype != MOE_DT_F16 && dtype != MOE_DT_BF16) return MOE_ERR_DTYPE;
+  if (R <= 0 || C <= 0 || E_glu <= 0 || R >= (1 << 30) || C >= (1 << 30)) return MOE_ERR_SHAPE;
+  if (!rsrc || !csrc || !offsets || !out) return MOE_ERR_SHAPE;
+  if (R % 8 != 0 || r_ld % 8 != 0 || c_ld % 8 != 0 || C % 4 != 0) return MOE_ERR_ALIGN;
+  if (!aligned16(rsrc) || !aligned16(csrc) || !aligned16(out)) return MOE_ERR_ALIGN;
+  WgradArgs a = {};
+  a.rsrc = rsrc; a.r_ld = r_ld; a.r_gather = r_gather;
+  a.csrc = csrc; a.c_ld = c_ld; a.c_gather = c_gather;
+  a.R = (int)R; a.C = (int)C; a.offsets = offsets; a.out = out;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&]<typename T>() {
+    using Cc = WgCfg<T>;
+    a.n_rtiles = (int)((R + Cc::BR - 1) / Cc::BR);
+    a.n_ctiles = (int)((C + Cc::BC - 1) / Cc::BC);
+    return launch_wgrad<Cc>(a, E_glu, s);
+  };
+  switch (dtype) {
+    case MOE_DT_BF16: return go.template operator()<bf16>();
+    case MOE_DT_F16: return go.template operator()<f16>();
+    default: return go.template operator()<float>();
+  }
+}

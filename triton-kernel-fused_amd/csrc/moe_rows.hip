@@ -1,0 +1,453 @@
+// Memory-bound row kernels of the MoE pipeline: the gate-weighted combine, its backward, the
+// un-permute of the input gradient, and the row-wise PolyGLU activation (BatchedGLU) forward and
+// backward for every activation code.
+//
+// Combine and un-permute are gathers, not scatters: one wave owns one token and sums its k routed
+// rows in slot order in fp32, so results are deterministic and need no atomics (the reference
+// scatters with fp32 atomics or index_add_, /root/reference/kernels/sm75/moe.py:673-682,593-595).
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int ROW_THREADS = 256;  // 4 waves, one token / routed row per wave
+
+template <typename T> struct Vec8;  // 16 bytes of T as floats
+template <> struct Vec8<bf16> {
+  static constexpr int N = 8;
+  // bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 bits.
+  __device__ __forceinline__ static void ld(const bf16* p, float* v) {
+    const uint4 u = *(const uint4*)p;
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static void st(bf16* p, const float* v) {
+    unsigned w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x2 t = {(bf16)v[2 * i], (bf16)v[2 * i + 1]};
+      w[i] = __builtin_bit_cast(unsigned, t);
+    }
+    *(uint4*)p = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <> struct Vec8<f16> {
+  static constexpr int N = 8;
+  typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
+  __device__ __forceinline__ static void ld(const f16* p, float* v) {
+    const uint4 u = *(const uint4*)p;
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h2 t = __builtin_bit_cast(h2, w[i]);
+      v[2 * i] = (float)t[0]; v[2 * i + 1] = (float)t[1];
+    }
+  }
+  __device__ __forceinline__ static void st(f16* p, const float* v) {
+    unsigned w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h2 t = {(f16)v[2 * i], (f16)v[2 * i + 1]};
+      w[i] = __builtin_bit_cast(unsigned, t);
+    }
+    *(uint4*)p = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <> struct Vec8<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void ld(const float* p, float* v) {
+    f32x4 u = *(const f32x4*)p;
+    v[0] = u[0]; v[1] = u[1]; v[2] = u[2]; v[3] = u[3];
+  }
+  __device__ __forceinline__ static void st(float* p, const float* v) {
+    *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// Kind of routed slot: 0 = GLU expert row, 1 = Identity (code 3), 2 = Zero (code 4) or invalid.
+__device__ __forceinline__ int slot_kind(int64_t e, const int32_t* codes, int E_glu, int E_all,
+                                         int pos) {
+  if (e < 0 || e >= E_all || pos < 0) return 2;
+  if (e < E_glu) return 0;
+  const int c = codes[e];
+  return c == 3 ? 1 : 2;
+}
+
+// out[t] = sum_j w[t,j] * row(t,j)
+template <typename T>
+__global__ void __launch_bounds__(ROW_THREADS)
+combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
+                   const T* __restrict__ wt, const int64_t* __restrict__ idx,
+                   const int32_t* __restrict__ codes, int E_glu, int E_all,
+                   const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
+  if (t >= N) return;
+  const int lane = threadIdx.x & 63;
+  for (int c = lane * V; c < H; c += 64 * V) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int64_t f = t * k + j;
+      const int pos = f2s[f];
+      const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+      if (kind == 2) continue;
+      const float w = to_f32(wt[f]);
+      float v[V];
+      if (kind == 0) Vec8<T>::ld(eo + (size_t)pos * H + c, v);
+      else Vec8<T>::ld(hidden + (size_t)t * H + c, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += w * v[i];
+    }
+    Vec8<T>::st(out + (size_t)t * H + c, acc);
+  }
+}
+
+// Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
+template <typename T>
+__global__ void __launch_bounds__(ROW_THREADS)
+combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict__ eo,
+                   const T* __restrict__ hidden, const T* __restrict__ wt,
+                   const int64_t* __restrict__ idx, const int32_t* __restrict__ codes, int E_glu,
+                   int E_all, const int32_t* __restrict__ st, const int32_t* __restrict__ sflat,
+                   int64_t M, int H, T* __restrict__ grad_eo, T* __restrict__ grad_wt) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t r = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
+  if (r >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int t = st[r];
+  const int f = sflat[r];
+  const int kind = slot_kind(idx[f], codes, E_glu, E_all, 0);
+  const float w = to_f32(wt[f]);
+  float dot = 0.f;
+  for (int c = lane * V; c < H; c += 64 * V) {
+    float g[V], v[V];
+    Vec8<T>::ld(go + (size_t)t * go_ld + c, g);
+    if (kind == 0) {
+      Vec8<T>::ld(eo + (size_t)r * H + c, v);
+      float ge[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) ge[i] = g[i] * w;
+      Vec8<T>::st(grad_eo + (size_t)r * H + c, ge);
+    } else if (kind == 1) {
+      Vec8<T>::ld(hidden + (size_t)t * H + c, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) dot += g[i] * v[i];
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) grad_wt[f] = from_f32<T>(dot);
+}
+
+// grad_x[t] = sum_j (GLU: grad_xs[pos]; Identity: w*go[t]; Zero: 0)
+template <typename T>
+__global__ void __launch_bounds__(ROW_THREADS)
+unpermute_bwd_kernel(const T* __restrict__ gxs, const T* __restrict__ go, int64_t go_ld,
+                     const T* __restrict__ wt, const int64_t* __restrict__ idx,
+                     const int32_t* __restrict__ codes, int E_glu, int E_all,
+                     const int32_t* __restrict__ f2s, int64_t N, int k, int H,
+                     T* __restrict__ gx) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
+  if (t >= N) return;
+  const int lane = threadIdx.x & 63;
+  for (int c = lane * V; c < H; c += 64 * V) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int64_t f = t * k + j;
+      const int pos = f2s[f];
+      const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+      if (kind == 2) continue;
+      float v[V];
+      if (kind == 0) {
+        Vec8<T>::ld(gxs + (size_t)pos * H + c, v);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += v[i];
+      } else {
+        const float w = to_f32(wt[f]);
+        Vec8<T>::ld(go + (size_t)t * go_ld + c, v);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += w * v[i];
+      }
+    }
+    Vec8<T>::st(gx + (size_t)t * H + c, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Row-wise PolyGLU (kernels/sm75/moe.py:163-232): one workgroup per row, the full intermediate
+// row in one pass, so the RMS of codes 2/6/7, the RMS-coupling sum S of their backward and the
+// SiTU parameter sums are block reductions in the same kernel.
+constexpr float NS_EPS = 1e-6f;
+constexpr int GLU_THREADS = 256;
+
+__device__ __forceinline__ float tanh_via_sigmoid(float x) { return 2.f / (1.f + __expf(-2.f * x)) - 1.f; }
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < GLU_THREADS / 64; ++w) s += red[w];
+  return s;
+}
+
+__device__ __forceinline__ bool is_norm_code(int c) { return c == 2 || c == 6 || c == 7; }
+
+template <typename T>
+__global__ void __launch_bounds__(GLU_THREADS)
+glu_fwd_kernel(const T* __restrict__ gu, int64_t gu_ld, const int32_t* __restrict__ row_act,
+               const float* __restrict__ alpha, const float* __restrict__ gamma, int ap_stride,
+               int I, T* __restrict__ out, int64_t out_ld) {
+  __shared__ float red[GLU_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const T* g = gu + row * gu_ld;
+  const T* u = g + I;
+  const int code = row_act[row];
+  const float aa = alpha ? alpha[row * ap_stride] : 1.f;
+  const float gg = gamma ? gamma[row * ap_stride] : 1.f;
+  float r = 1.f;
+  if (is_norm_code(code)) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < I; i += GLU_THREADS) { float x = to_f32(g[i]); ss += x * x; }
+    ss = block_sum(ss, red);
+    r = sqrtf(ss / I + NS_EPS);
+  }
+  for (int i = threadIdx.x; i < I; i += GLU_THREADS) {
+    const float gate = to_f32(g[i]);
+    const float up = to_f32(u[i]);
+    const float gn = is_norm_code(code) ? gate / r : gate;
+    const float sig = sigmoid(gn);
+    float act;
+    if (code == 1 || code == 6) { float rl = fmaxf(gn, 0.f); act = rl * rl; }
+    else if (code == 5) act = gg * tanh_via_sigmoid(aa * gate) * sig;
+    else if (code == 7) act = tanh_via_sigmoid(gn) * sig;
+    else act = gn * sig;  // codes 0, 2
+    out[row * out_ld + i] = from_f32<T>(act * up);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(GLU_THREADS)
+glu_bwd_kernel(const T* __restrict__ go_, int64_t go_rs, int64_t go_cs, const T* __restrict__ gu,
+               int64_t gu_ld, const int32_t* __restrict__ row_act,
+               const float* __restrict__ alpha, const float* __restrict__ gamma, int ap_stride,
+               int I, T* __restrict__ ggu, int64_t ggu_ld, float* __restrict__ da,
+               float* __restrict__ dg) {
+  __shared__ float red[GLU_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const T* g = gu + row * gu_ld;
+  const T* u = g + I;
+  const T* gop = go_ + row * go_rs;
+  const int code = row_act[row];
+  const bool norm = is_norm_code(code);
+  const float aa = alpha ? alpha[row * ap_stride] : 1.f;
+  const float gg = gamma ? gamma[row * ap_stride] : 1.f;
+  float r = 1.f, S = 0.f;
+  if (norm) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < I; i += GLU_THREADS) { float x = to_f32(g[i]); ss += x * x; }
+    ss = block_sum(ss, red);
+    r = sqrtf(ss / I + NS_EPS);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < I; i += GLU_THREADS) {
+      const float gn = to_f32(g[i]) / r;
+      const float sig = sigmoid(gn);
+      float df;
+      if (code == 6) df = 2.f * fmaxf(gn, 0.f);
+      else if (code == 7) { float tg = tanh_via_sigmoid(gn); df = (1.f - tg * tg) * sig + tg * sig * (1.f - sig); }
+      else df = sig * (1.f + gn * (1.f - sig));
+      s += to_f32(gop[i * go_cs]) * to_f32(u[i]) * df * gn;
+    }
+    S = block_sum(s, red);
+  }
+  float sda = 0.f, sdg = 0.f;
+  for (int i = threadIdx.x; i < I; i += GLU_THREADS) {
+    const float gate = to_f32(g[i]);
+    const float up = to_f32(u[i]);
+    const float go = to_f32(gop[i * go_cs]);
+    const float gn = norm ? gate / r : gate;
+    const float sig = sigmoid(gn);
+    const float gup = go * up;
+    float act, grad_gate;
+    if (code == 1) {
+      float rl = fmaxf(gn, 0.f); act = rl * rl; grad_gate = gup * 2.f * rl;
+    } else if (code == 5) {
+      const float t5 = tanh_via_sigmoid(aa * gate);
+      act = gg * t5 * sig;
+      grad_gate = gup * gg * (aa * (1.f - t5 * t5) * sig + t5 * sig * (1.f - sig));
+      sda += gup * gg * gate * (1.f - t5 * t5) * sig;
+      sdg += gup * t5 * sig;
+    } else if (norm) {
+      float df;
+      if (code == 6) { float rl = fmaxf(gn, 0.f); act = rl * rl; df = 2.f * rl; }
+      else if (code == 7) { float tg = tanh_via_sigmoid(gn); act = tg * sig; df = (1.f - tg * tg) * sig + tg * sig * (1.f - sig); }
+      else { act = gn * sig; df = sig * (1.f + gn * (1.f - sig)); }
+      grad_gate = (gup * df - (S / I) * gn) / r;
+    } else {  // code 0
+      act = gn * sig;
+      grad_gate = gup * sig * (1.f + gn * (1.f - sig));
+    }
+    ggu[row * ggu_ld + i] = from_f32<T>(grad_gate);
+    ggu[row * ggu_ld + I + i] = from_f32<T>(go * act);
+  }
+  if (da) {
+    sda = block_sum(sda, red);
+    sdg = block_sum(sdg, red);
+    if (threadIdx.x == 0) {
+      da[row] = code == 5 ? sda : 0.f;
+      dg[row] = code == 5 ? sdg : 0.f;
+    }
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+static int vec_of(int dtype) { return dtype == MOE_DT_F32 ? 4 : 8; }
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Launch KERNEL<T_> with T_ bound to the element type of `dtype` (the argument list may use T_).
+#define MOE_BY_DTYPE(dtype, KERNEL, GRID, BLOCK, STREAM, ...)      \
+  do {                                                             \
+    if ((dtype) == MOE_DT_BF16) {                                  \
+      typedef bf16 T_;                                             \
+      hipLaunchKernelGGL(KERNEL<T_>, GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    } else if ((dtype) == MOE_DT_F16) {                            \
+      typedef f16 T_;                                              \
+      hipLaunchKernelGGL(KERNEL<T_>, GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    } else {                                                       \
+      typedef float T_;                                            \
+      hipLaunchKernelGGL(KERNEL<T_>, GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    }                                                              \
+  } while (0)
+
+static int check_rows(int dtype, int64_t n, int top_k, int64_t H, int n_experts, int E_glu) {
+  if (dtype < 0 || dtype > 2) return MOE_ERR_DTYPE;
+  if (n < 0 || top_k <= 0 || H <= 0 || H >= (1 << 30) || n_experts <= 0 || E_glu < 0 ||
+      E_glu > n_experts)
+    return MOE_ERR_SHAPE;
+  if (H % vec_of(dtype)) return MOE_ERR_ALIGN;
+  return MOE_OK;
+}
+
+static unsigned row_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
+
+extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
+                               const void* top_k_weights, const int64_t* top_k_indices,
+                               const int32_t* act_codes, int n_experts, int E_glu,
+                               const int32_t* flat_to_sorted, int64_t n_tokens, int top_k,
+                               int64_t H, void* out, void* stream) {
+  int st = check_rows(dtype, n_tokens, top_k, H, n_experts, E_glu);
+  if (st) return st;
+  if (n_tokens == 0) return MOE_OK;
+  if (!hidden || !top_k_weights || !top_k_indices || !act_codes || !flat_to_sorted || !out ||
+      (E_glu > 0 && !eo))
+    return MOE_ERR_SHAPE;
+  if (!al16(hidden) || !al16(out) || (eo && !al16(eo))) return MOE_ERR_ALIGN;
+  if (row_grid(n_tokens) >= (1u << 31)) return MOE_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, combine_fwd_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
+               (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+               act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_combine_bwd(int dtype, const void* grad_out, int64_t grad_out_ld,
+                               const void* eo, const void* hidden, const void* top_k_weights,
+                               const int64_t* top_k_indices, const int32_t* act_codes,
+                               int n_experts, int E_glu, const int32_t* sorted_token,
+                               const int32_t* sorted_flat, int64_t n_rows, int top_k, int64_t H,
+                               void* grad_eo_out, void* grad_wt_out, void* stream) {
+  int st = check_rows(dtype, n_rows, top_k, H, n_experts, E_glu);
+  if (st) return st;
+  if (n_rows == 0) return MOE_OK;
+  if (!grad_out || !hidden || !top_k_weights || !top_k_indices || !act_codes || !sorted_token ||
+      !sorted_flat || !grad_wt_out || (E_glu > 0 && (!eo || !grad_eo_out)))
+    return MOE_ERR_SHAPE;
+  if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
+  if (!al16(grad_out) || !al16(hidden) || (eo && !al16(eo)) || (grad_eo_out && !al16(grad_eo_out)))
+    return MOE_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, combine_bwd_kernel, dim3(row_grid(n_rows)), dim3(ROW_THREADS), s,
+               (const T_*)grad_out, grad_out_ld, (const T_*)eo, (const T_*)hidden,
+               (const T_*)top_k_weights, top_k_indices, act_codes, E_glu, n_experts, sorted_token,
+               sorted_flat, n_rows, (int)H, (T_*)grad_eo_out, (T_*)grad_wt_out);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_unpermute_bwd(int dtype, const void* grad_xs, const void* grad_out,
+                                 int64_t grad_out_ld, const void* top_k_weights,
+                                 const int64_t* top_k_indices, const int32_t* act_codes,
+                                 int n_experts, int E_glu, const int32_t* flat_to_sorted,
+                                 int64_t n_tokens, int top_k, int64_t H, void* grad_x_out,
+                                 void* stream) {
+  int st = check_rows(dtype, n_tokens, top_k, H, n_experts, E_glu);
+  if (st) return st;
+  if (n_tokens == 0) return MOE_OK;
+  if (!grad_out || !top_k_weights || !top_k_indices || !act_codes || !flat_to_sorted ||
+      !grad_x_out || (E_glu > 0 && !grad_xs))
+    return MOE_ERR_SHAPE;
+  if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
+  if (!al16(grad_out) || !al16(grad_x_out) || (grad_xs && !al16(grad_xs))) return MOE_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, unpermute_bwd_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
+               (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
+               top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+               (int)H, (T_*)grad_x_out);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_glu_fwd(int dtype, const void* gate_up, int64_t gu_ld, const int32_t* row_act,
+                           const float* alpha, const float* gamma, int ap_stride, int64_t n_rows,
+                           int64_t I, void* out, int64_t out_ld, void* stream) {
+  if (dtype < 0 || dtype > 2) return MOE_ERR_DTYPE;
+  if (n_rows < 0 || I <= 0 || I >= (1 << 30) || gu_ld < 2 * I || out_ld < I) return MOE_ERR_SHAPE;
+  if (n_rows == 0) return MOE_OK;
+  if (!gate_up || !row_act || !out || n_rows >= (1ll << 31)) return MOE_ERR_SHAPE;
+  if ((alpha == nullptr) != (gamma == nullptr)) return MOE_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, glu_fwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
+               (const T_*)gate_up, gu_ld, row_act, alpha, gamma, ap_stride, (int)I, (T_*)out,
+               out_ld);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_glu_bwd(int dtype, const void* grad_out, int64_t go_row_stride,
+                           int64_t go_col_stride, const void* gate_up, int64_t gu_ld,
+                           const int32_t* row_act, const float* alpha, const float* gamma,
+                           int ap_stride, int64_t n_rows, int64_t I, void* ggu_out,
+                           int64_t ggu_ld, float* da_out, float* dg_out, void* stream) {
+  if (dtype < 0 || dtype > 2) return MOE_ERR_DTYPE;
+  if (n_rows < 0 || I <= 0 || I >= (1 << 30) || gu_ld < 2 * I || ggu_ld < 2 * I) return MOE_ERR_SHAPE;
+  if (n_rows == 0) return MOE_OK;
+  if (!grad_out || !gate_up || !row_act || !ggu_out || n_rows >= (1ll << 31)) return MOE_ERR_SHAPE;
+  if ((alpha == nullptr) != (gamma == nullptr) || (da_out == nullptr) != (dg_out == nullptr))
+    return MOE_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, glu_bwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
+               (const T_*)grad_out, go_row_stride, go_col_stride, (const T_*)gate_up, gu_ld,
+               row_act, alpha, gamma, ap_stride, (int)I, (T_*)ggu_out, ggu_ld, da_out, dg_out);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" const char* moe_version(void) { return "moe_gfx950 0.1.0"; }

@@ -1,0 +1,96 @@
+"""ctypes binding of libmoe_gfx950.so (the C ABI declared in include/moe_gfx950.h).
+
+Only plain pointers, integers and the HIP stream handle cross this boundary; PyTorch owns every
+buffer. A missing library is an error, never a fallback: the MoE entry points have no other
+implementation.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MOE_GFX950_LIB",
+                          os.path.join(os.path.dirname(_HERE), "libmoe_gfx950.so"))
+
+MOE_DT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_S = ctypes.c_size_t
+
+# name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
+_SIGS = {
+    "moe_version": [],
+    "moe_tile_rows": [],
+    "moe_get_workspace_size": [_L, _I, _I],
+    "moe_dispatch": [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
+    "moe_grouped_gateup_swiglu_fwd": [_I, _P, _L, _L, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P, _P],
+    "moe_grouped_down_fwd": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
+    "moe_combine_fwd": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
+    "moe_combine_bwd": [_I, _P, _L, _P, _P, _P, _P, _P, _I, _I, _P, _P, _L, _I, _L, _P, _P, _P],
+    "moe_grouped_down_dx_swiglu_bwd": [_I, _P, _P, _I, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P],
+    "moe_grouped_gateup_dx": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
+    "moe_grouped_wgrad": [_I, _P, _L, _P, _P, _L, _P, _L, _L, _P, _I, _P, _P],
+    "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
+    "moe_glu_fwd": [_I, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P],
+    "moe_glu_bwd": [_I, _P, _L, _L, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P],
+}
+_RESTYPES = {"moe_version": ctypes.c_char_p, "moe_get_workspace_size": ctypes.c_size_t}
+
+_ERRORS = {
+    1: (ValueError, "shape"),
+    2: (ValueError, "alignment (16-byte pointers; H and I multiples of 8)"),
+    3: (ValueError, "unsupported activation code"),
+    4: (TypeError, "dtype"),
+    5: (RuntimeError, "HIP launch failure"),
+    6: (ValueError, "workspace"),
+}
+
+_lib = None
+
+
+def declared_symbols():
+    return sorted(_SIGS)
+
+
+def lib():
+    """Load the library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python triton-kernel-fused_amd/build_lib.py` "
+                "(or __graft_entry__.build()); the MoE entry points have no fallback path")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in _SIGS.items():
+            fn = getattr(h, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = h
+    return _lib
+
+
+def call(name, *args):
+    """Call an int-status entry point and raise the mapped Python exception on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        exc, what = _ERRORS.get(rc, (RuntimeError, "unknown"))
+        raise exc(f"{name} failed: {what} (status {rc})")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt):
+    try:
+        return MOE_DT[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16") from None

@@ -1,0 +1,4 @@
+"""Import-path alias: `from kernels.sm75 import moe` resolves to the gfx950 implementation."""
+from ..gfx950 import moe, moe_per_expert, moe_eager  # noqa: F401
+
+__all__ = ["moe", "moe_per_expert", "moe_eager"]
