@@ -1,0 +1,192 @@
+"""Benchmark of the gfx950 MoE layer (one GPU). Prints ONE JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--config 3] [--no-cpu] [--no-extra]
+
+Workload (value): BASELINE config 3 — bf16 MoE layer fwd+bwd, N=16384 tokens, d_model=2048,
+d_ff=1024, E=64 SwiGLU experts, top-8 sigmoid routing with log-Zipf expert bias (imbalanced, some
+experts empty). One step = dispatch + grouped gate/up GEMM with SwiGLU + grouped down GEMM +
+combine, then the full backward (combine bwd, down dX + SwiGLU bwd, both wgrads, gate/up dX,
+un-permute) for every input and weight, with inputs already resident in HBM.
+value = algorithmic TFLOP/s = 18*M*H*I / step time (M = N*k routed rows; forward 6*M*H*I,
+backward 12*M*H*I; routing, elementwise and scatter work excluded).
+
+Extra fields beside the contract: per-kernel HIP-event timings over the timed region ("kernels"),
+the roofline of the dominant kernel ("roofline"), the CPU baseline ("cpu_baseline") and the
+other bf16 config ("extra_configs").
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "triton-kernel-fused_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE layer TFLOP/s (bf16 fwd+bwd, fp8/MXFP8 fwd) and % of MI355X MFMA/HBM peak"
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense fp8 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+
+# algorithmic FLOPs per call of each entry point, in units of M*H*I (M = routed GLU rows)
+KERNEL_MHI = {
+    "moe_grouped_gateup_swiglu_fwd": 4, "moe_grouped_down_fwd": 2,
+    "moe_grouped_down_dx_swiglu_bwd": 2, "moe_grouped_gateup_dx": 4,
+    "moe_grouped_wgrad:down": 2, "moe_grouped_wgrad:gate_up": 4,
+}
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[workload][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def run_bf16(config, steps, warmup, timer=True):
+    import torch
+    import kernels
+    from kernels import _lib
+    from kernels.workloads import make_workload, flops
+
+    wl = make_workload(config, device="cuda", seed=0)
+    cfg = wl["cfg"]
+    leaves = [wl[k].detach().requires_grad_(True) for k in ("hidden", "wt", "gate_up_proj", "down_proj")]
+    idx, codes, dy = wl["idx"], wl["act_codes"], wl["grad_out"]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        out = kernels.moe(leaves[0], idx, leaves[1], leaves[2], leaves[3], codes)
+        out.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    records = []
+    if timer:
+        _lib.set_timer(records)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.set_timer(None)
+    ms = (t1 - t0) * 1e3 / steps
+    f = flops(cfg)
+    m = cfg["N"] * cfg["k"]
+    mhi = m * cfg["H"] * cfg["I"]
+    per = {}
+    for name, e0, e1 in records:
+        per.setdefault(name, []).append(e0.elapsed_time(e1))
+    kern = {}
+    for name, ts in per.items():
+        avg = statistics.mean(ts)
+        d = {"ms": round(avg, 4), "calls_per_step": len(ts) // steps}
+        if name in KERNEL_MHI:
+            tf = KERNEL_MHI[name] * mhi / (avg * 1e-3) / 1e12
+            d.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        kern[name] = d
+    return dict(cfg=cfg, ms=ms, tflops=f / (ms * 1e-3) / 1e12, kernels=kern, mhi=mhi)
+
+
+def cpu_baseline(config, sample_tokens, reps=3):
+    """The oracle's fp32 eager MoE fwd+bwd (a restatement of the reference moe_eager, PyTorch on
+    the host cores), on the first `sample_tokens` tokens of the same workload."""
+    import torch
+    from kernels.workloads import make_workload, flops
+    from oracle import moe_oracle as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    wl = make_workload(config, device="cpu", seed=0, gen_device="cpu",
+                       scale=dict(N=sample_tokens))
+    cfg = wl["cfg"]
+    args = [wl[k].float() for k in ("hidden", "idx", "wt", "gate_up_proj", "down_proj")]
+    args[1] = wl["idx"]
+    times = []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        orc.moe_fwd_bwd(*args, [0] * cfg["E"], wl["grad_out"].float())
+        dt = time.perf_counter() - t0
+        if r:
+            times.append(dt)
+        _log(f"cpu rep {r}: {dt:.2f}s")
+    med = statistics.median(times)
+    f = flops(cfg)
+    return {"value": round(f / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"config {config} routing/weights with N={sample_tokens} tokens "
+                       f"(M={sample_tokens * cfg['k']} rows), fp32 fwd+bwd, median of {reps} after 1 "
+                       f"warmup; os.cpu_count()={os.cpu_count()}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=1024)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (all experts resident, "
+              "no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs the GPU", file=sys.stderr)
+        sys.exit(1)
+
+    _log(f"config {args.config}: warmup {args.warmup}, steps {args.steps}")
+    r = run_bf16(args.config, args.steps, args.warmup)
+    cfg = r["cfg"]
+    kern = r["kernels"]
+    gemms = {k: v for k, v in kern.items() if k in KERNEL_MHI}
+    dom = max(gemms, key=lambda k: gemms[k]["ms"])
+    wl_name = cfg["name"]
+    achieved = gemms[dom]["tflops"]
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": _traffic(dom, wl_name),
+                "flops_per_launch": KERNEL_MHI[dom] * r["mhi"]}
+    line = {
+        "metric": METRIC, "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; random-init weights of the config's shapes)",
+        "config": {"workload": (f"{wl_name}: bf16 MoE layer fwd+bwd N={cfg['N']} H={cfg['H']} "
+                                f"I={cfg['I']} E={cfg['E']} k={cfg['k']} SwiGLU"),
+                   "global_batch": cfg["N"], "seq_len": None, "parallelism": "single GPU"},
+        "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "roofline": roofline, "kernels": kern,
+    }
+    if not args.no_extra:
+        other = 2 if args.config != 2 else 3
+        _log(f"extra config {other}")
+        r2 = run_bf16(other, max(5, args.steps // 2), 2, timer=False)
+        line["extra_configs"] = {r2["cfg"]["name"]: {"tflops": round(r2["tflops"], 2),
+                                                     "ms_per_step": round(r2["ms"], 4),
+                                                     "frac_of_peak": round(r2["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+    if not args.no_cpu:
+        _log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -49,6 +49,14 @@ _ERRORS = {
 }
 
 _lib = None
+_timer = None   # list collecting (name, start_event, end_event) while a bench times kernels
+
+
+def set_timer(records):
+    """Record a HIP event pair around every entry-point call into `records` (a list), on the
+    stream the library launches on (torch's current stream); None switches it off."""
+    global _timer
+    _timer = records
 
 
 def declared_symbols():
@@ -72,9 +80,17 @@ def lib():
     return _lib
 
 
-def call(name, *args):
-    """Call an int-status entry point and raise the mapped Python exception on failure."""
-    rc = getattr(lib(), name)(*args)
+def call(name, *args, tag=None):
+    """Call an int-status entry point and raise the mapped Python exception on failure. `tag`
+    only labels the call in timer records (e.g. which weight a wgrad is for)."""
+    if _timer is None:
+        rc = getattr(lib(), name)(*args)
+    else:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        rc = getattr(lib(), name)(*args)
+        ev1.record()
+        _timer.append((name if tag is None else f"{name}:{tag}", ev0, ev1))
     if rc != 0:
         exc, what = _ERRORS.get(rc, (RuntimeError, "unknown"))
         raise exc(f"{name} failed: {what} (status {rc})")

@@ -264,12 +264,12 @@ class _MoEFunction(torch.autograd.Function):
                 g_dw = torch.empty_like(down_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(inter), inter_dim, None,
                           _lib.ptr(grad_eo), h, None, inter_dim, h, _lib.ptr(routing.offsets),
-                          e_glu, _lib.ptr(g_dw), stream)
+                          e_glu, _lib.ptr(g_dw), stream, tag="down")
             if need_gu:
                 g_gu = torch.empty_like(gate_up_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(hidden), h,
                           _lib.ptr(routing.sorted_token), _lib.ptr(ggu), two_i, None, h, two_i,
-                          _lib.ptr(routing.offsets), e_glu, _lib.ptr(g_gu), stream)
+                          _lib.ptr(routing.offsets), e_glu, _lib.ptr(g_gu), stream, tag="gate_up")
         elif e_glu > 0:
             if need_dw:
                 g_dw = torch.zeros_like(down_proj)
