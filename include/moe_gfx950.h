@@ -50,13 +50,14 @@ size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_experts);
  * Replaces `_sort_by_expert` (kernels/sm75/moe.py:564-572), `_build_schedule` (:535-543) and the
  * sort / bincount / cumsum of kernels/sm120/moe_grouped.py:94-100, with no host sync.
  * Outputs: counts[E], offsets[E+1] (exclusive prefix of counts), tile_offsets[E+1] (exclusive
- * prefix of ceil(counts/moe_tile_rows())), sorted_token[M] (token id t of each sorted row),
+ * prefix of ceil(counts/moe_tile_rows())), expert_order[E] (expert ids by descending count, ties
+ * by id), sorted_token[M] (token id t of each sorted row),
  * sorted_flat[M] (flat index t*k+j of each sorted row), flat_to_sorted[M] (inverse permutation;
  * -1 for an index outside [0, E)), status[0] += number of such out-of-range indices. */
 int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int n_experts,
-                 int32_t* counts, int32_t* offsets, int32_t* tile_offsets, int32_t* sorted_token,
-                 int32_t* sorted_flat, int32_t* flat_to_sorted, int32_t* status, void* workspace,
-                 size_t workspace_bytes, void* stream);
+                 int32_t* counts, int32_t* offsets, int32_t* tile_offsets, int32_t* expert_order,
+                 int32_t* sorted_token, int32_t* sorted_flat, int32_t* flat_to_sorted,
+                 int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grouped gate/up projection with the GLU epilogue.
  * gate_up[m] = hidden[sorted_token[m]] @ gate_up_proj[e]^T for every sorted row m of a GLU expert
@@ -120,6 +121,8 @@ int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj, 
  *   out[e, c, r] = sum_m  rsrc[rrow(m), r] * csrc[crow(m), c]
  * rrow(m) = r_gather ? r_gather[m] : m (same for c). Rows of rsrc are r_ld elements apart, rows of
  * csrc c_ld apart. out is (E_glu, C, R) contiguous; experts with no rows get zeros.
+ * expert_order (optional, from moe_dispatch, n_experts entries) lists the experts by descending
+ * row count so the longest reductions are scheduled first; entries >= E_glu are skipped.
  * down:    out = grad_down_proj (E,H,I): rsrc = inter (R=I), csrc = grad_eo (C=H).
  * gate_up: out = grad_gate_up_proj (E,2I,H): rsrc = hidden gathered by sorted_token (R=H),
  *          csrc = ggu (C=2I).
@@ -127,7 +130,8 @@ int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj, 
  * `ge.t() @ it`, `grad_gate_up.t() @ x_s[s:en]` (:808,821). */
 int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
                       const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R, int64_t C,
-                      const int32_t* offsets, int E_glu, void* out, void* stream);
+                      const int32_t* offsets, const int32_t* expert_order, int n_experts, int E_glu,
+                      void* out, void* stream);
 
 /* Un-permute backward: grad_x[t] = sum_j contribution(t,j) in slot order, fp32 accumulation;
  * contribution = grad_xs[flat_to_sorted[t*k+j]] (GLU), w * grad_out[t] (Identity), 0 (Zero).

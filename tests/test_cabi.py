@@ -45,10 +45,11 @@ def test_workspace_size():
 # Argument validation happens on the host before any HIP call, so these run without a GPU.
 def test_dispatch_rejects_bad_arguments():
     h = _lib.lib()
-    assert h.moe_dispatch(None, 4, 2, 0, None, None, None, None, None, None, None, None, 0, None) == 1
-    assert h.moe_dispatch(None, 4, 2, 2000, None, None, None, None, None, None, None, None, 0, None) == 1
+    nul = [None] * 8
+    assert h.moe_dispatch(None, 4, 2, 0, *nul, None, 0, None) == 1
+    assert h.moe_dispatch(None, 4, 2, 2000, *nul, None, 0, None) == 1
     fake = ctypes.c_void_p(16)
-    assert h.moe_dispatch(fake, 4, 2, 8, fake, fake, fake, fake, fake, fake, fake, None, 0, None) == 6
+    assert h.moe_dispatch(fake, 4, 2, 8, *([fake] * 8), None, 0, None) == 6
 
 
 def test_gemm_entry_points_reject_bad_arguments():
@@ -64,7 +65,8 @@ def test_gemm_entry_points_reject_bad_arguments():
     assert h.moe_grouped_down_fwd(2, fake, fake, 0, 64, 64, fake, None, 10, fake, None) == 1
     # zero rows is a no-op success
     assert h.moe_grouped_down_fwd(2, fake, fake, 4, 64, 64, fake, None, 0, fake, None) == 0
-    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, 4, fake, None) == 2
+    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, None, 4, 4, fake, None) == 2
+    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 64, None, 64, 64, fake, fake, 3, 4, fake, None) == 1
     assert h.moe_combine_fwd(2, fake, fake, fake, fake, fake, 4, 5, fake, 10, 2, 64, fake, None) == 1
     assert h.moe_glu_fwd(2, fake, 10, fake, fake, None, 1, 4, 8, fake, 8, None) == 1
 

@@ -25,6 +25,8 @@ def _check(idx_cpu, n_experts):
     np.testing.assert_array_equal(r.offsets.cpu().numpy(), ref["offsets"])
     np.testing.assert_array_equal(r.tile_offsets.cpu().numpy(),
                                   orc.tile_offsets(ref["counts"], _lib.lib().moe_tile_rows()))
+    np.testing.assert_array_equal(r.expert_order.cpu().numpy(),
+                                  np.argsort(-ref["counts"], kind="stable"))
     n_valid = int(ref["offsets"][-1])
     np.testing.assert_array_equal(r.sorted_flat.cpu().numpy()[:n_valid], ref["sorted_flat"])
     np.testing.assert_array_equal(r.sorted_token.cpu().numpy()[:n_valid], ref["sorted_token"])

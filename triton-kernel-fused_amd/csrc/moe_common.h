@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/moe_gfx950.h"
 
 namespace moe {
@@ -73,6 +75,16 @@ __device__ __forceinline__ i32x4 zero4() { return i32x4{0, 0, 0, 0}; }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
 __device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [I, N). Each iteration is its own
+// code instance, so arrays indexed by the loop variable stay in registers however large the body.
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
 
 // 64-bit wave ballot.
 __device__ __forceinline__ unsigned long long ballot64(bool p) { return __ballot(p); }

@@ -51,7 +51,8 @@ dispatch_hist_kernel(const int64_t* __restrict__ idx, int64_t M, int E, int32_t*
 // One workgroup. hist (nchunks, E) is rewritten in place into exclusive per-chunk bases.
 __global__ void __launch_bounds__(1024)
 dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E, int32_t* __restrict__ counts,
-                     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets) {
+                     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets,
+                     int32_t* __restrict__ expert_order) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
   const int e = threadIdx.x;
@@ -67,6 +68,16 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E, int32_t* __
     s_tiles[e] = (run + TILE_ROWS - 1) / TILE_ROWS;
   }
   __syncthreads();
+  // Experts by descending count (ties by id): rank = experts that sort before this one.
+  if (e < E) {
+    const int c = s_cnt[e];
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+      const int cj = s_cnt[j];
+      rank += (cj > c) || (cj == c && j < e);
+    }
+    expert_order[rank] = e;
+  }
   // E <= 1024: a serial scan by one thread is a few microseconds at most and keeps this exact.
   if (threadIdx.x == 0) {
     int o = 0, t = 0;
@@ -160,13 +171,13 @@ extern "C" size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_expe
 
 extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
                             int n_experts, int32_t* counts, int32_t* offsets,
-                            int32_t* tile_offsets, int32_t* sorted_token, int32_t* sorted_flat,
-                            int32_t* flat_to_sorted, int32_t* status, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+                            int32_t* tile_offsets, int32_t* expert_order, int32_t* sorted_token,
+                            int32_t* sorted_flat, int32_t* flat_to_sorted, int32_t* status,
+                            void* workspace, size_t workspace_bytes, void* stream) {
   if (n_tokens < 0 || top_k <= 0 || n_experts <= 0 || n_experts > MAX_EXPERTS) return MOE_ERR_SHAPE;
   const int64_t M = n_tokens * top_k;
   if (M >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  if (!counts || !offsets || !tile_offsets || !status) return MOE_ERR_SHAPE;
+  if (!counts || !offsets || !tile_offsets || !expert_order || !status) return MOE_ERR_SHAPE;
   if (M > 0 && (!top_k_indices || !sorted_token || !sorted_flat || !flat_to_sorted))
     return MOE_ERR_SHAPE;
   if (!workspace || workspace_bytes < moe_get_workspace_size(n_tokens, top_k, n_experts))
@@ -179,7 +190,7 @@ extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int 
                        M, n_experts, hist, status);
   }
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, nc, n_experts, counts,
-                     offsets, tile_offsets);
+                     offsets, tile_offsets, expert_order);
   if (nc > 0) {
     hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s,
                        top_k_indices, M, top_k, n_experts, hist, offsets, sorted_token,

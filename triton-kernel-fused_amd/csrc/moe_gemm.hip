@@ -14,6 +14,7 @@
 // prefix from the dispatch offsets in LDS (a block scan), finds its expert by binary search and
 // exits if its tile is past the end, so the grid is a host-side upper bound and nothing syncs.
 #include "moe_common.h"
+#include "moe_gemm_v2.h"
 
 namespace moe {
 
@@ -297,6 +298,92 @@ __device__ __forceinline__ void tile_prefix(const int32_t* offsets, int E, int B
   __syncthreads();
 }
 
+// Token-GEMM epilogue: acc holds P rows x token columns of tile (rt, sorted rows m0..) of expert e.
+template <class C, int EPI>
+__device__ __forceinline__ void token_epilogue(f32x16 (&acc)[C::TI][C::TJ], const TokenArgs& a, int e,
+                                               int m0, int m_end, int rt) {
+  typedef typename C::T T;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int h = lane >> 5;
+  // act_codes is NULL when the epilogue only writes raw GEMM results (grad_inter mode).
+  const int code = (EPI == EPI_STORE || a.act_codes == nullptr) ? 0 : a.act_codes[e];
+  static_for<0, C::TJ>([&](auto tj_c) {
+    constexpr int tj = decltype(tj_c)::value;
+    const int m = m0 + wc * C::WTC + tj * 32 + (lane & 31);
+    if (m >= m_end) return;
+    if constexpr (EPI == EPI_STORE) {
+      T* o = (T*)a.out + (size_t)m * a.out_ld;
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+          if (r < a.R)
+            Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1],
+                          acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3]);
+        }
+    } else if constexpr (EPI == EPI_GLU_FWD) {
+      T* gu = (T*)a.out + (size_t)m * 2 * a.I;
+      T* it = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
+#pragma unroll
+      for (int ti = 0; ti < C::TI / 2; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + ti * 32 + 8 * g + 4 * h;
+          if (ch >= a.I) continue;
+          float gv[4], uv[4], iv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            gv[j] = round_through<T>(acc[ti][tj][4 * g + j]);
+            uv[j] = round_through<T>(acc[ti + C::TI / 2][tj][4 * g + j]);
+            iv[j] = glu_act(code, gv[j]) * uv[j];
+          }
+          Store4<T>::st(gu + ch, gv[0], gv[1], gv[2], gv[3]);
+          Store4<T>::st(gu + a.I + ch, uv[0], uv[1], uv[2], uv[3]);
+          if (it) Store4<T>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
+        }
+    } else {  // EPI_GLU_BWD: acc = grad_inter[m, i]
+      const T* gu = (const T*)a.aux + (size_t)m * 2 * a.I;
+      T* ggu = a.out ? (T*)a.out + (size_t)m * 2 * a.I : nullptr;
+      T* gi = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti) {
+        // The gate/up values of this lane's 16 channels in tile row ti, loaded together.
+        float gv[4][4], uv[4][4];
+        const int ib = rt * C::BR + wr * C::WTR + ti * 32 + 4 * h;
+        if (ggu) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int i0 = min(ib + 8 * g, a.I - 4);
+            Store4<T>::ld(gu + i0, gv[g]);
+            Store4<T>::ld(gu + a.I + i0, uv[g]);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i0 = ib + 8 * g;
+          float go[4], dg[4], du[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            go[j] = round_through<T>(acc[ti][tj][4 * g + j]);
+            dg[j] = go[j] * uv[g][j] * glu_dact(code, gv[g][j]);
+            du[j] = go[j] * glu_act(code, gv[g][j]);
+          }
+          if (i0 < a.I) {
+            if (gi) Store4<T>::st(gi + i0, go[0], go[1], go[2], go[3]);
+            if (ggu) {
+              Store4<T>::st(ggu + i0, dg[0], dg[1], dg[2], dg[3]);
+              Store4<T>::st(ggu + a.I + i0, du[0], du[1], du[2], du[3]);
+            }
+          }
+        }
+      }
+    }
+  });
+}
+
 template <class C, int EPI, bool P_RC>
 __global__ void __launch_bounds__(C::NT)
 token_gemm_kernel(TokenArgs a) {
@@ -379,76 +466,7 @@ token_gemm_kernel(TokenArgs a) {
     mainloop<C>(acc, lp, lq, 0, a.K, smem);
   }
 
-  // Epilogue.
-  const int lane = tid & 63, wid = tid >> 6;
-  const int wr = wid / C::WC, wc = wid % C::WC;
-  const int h = lane >> 5;
-  // act_codes is NULL when the epilogue only writes raw GEMM results (grad_inter mode).
-  const int code = (EPI == EPI_STORE || a.act_codes == nullptr) ? 0 : a.act_codes[e];
-#pragma unroll
-  for (int tj = 0; tj < C::TJ; ++tj) {
-    const int m = m0 + wc * C::WTC + tj * 32 + (lane & 31);
-    if (m >= m_end) continue;
-    if constexpr (EPI == EPI_STORE) {
-      T* o = (T*)a.out + (size_t)m * a.out_ld;
-#pragma unroll
-      for (int ti = 0; ti < C::TI; ++ti)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int r = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
-          if (r < a.R)
-            Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1],
-                          acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3]);
-        }
-    } else if constexpr (EPI == EPI_GLU_FWD) {
-      T* gu = (T*)a.out + (size_t)m * 2 * a.I;
-      T* it = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
-#pragma unroll
-      for (int ti = 0; ti < C::TI / 2; ++ti)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + ti * 32 + 8 * g + 4 * h;
-          if (ch >= a.I) continue;
-          float gv[4], uv[4], iv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            gv[j] = round_through<T>(acc[ti][tj][4 * g + j]);
-            uv[j] = round_through<T>(acc[ti + C::TI / 2][tj][4 * g + j]);
-            iv[j] = glu_act(code, gv[j]) * uv[j];
-          }
-          Store4<T>::st(gu + ch, gv[0], gv[1], gv[2], gv[3]);
-          Store4<T>::st(gu + a.I + ch, uv[0], uv[1], uv[2], uv[3]);
-          if (it) Store4<T>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
-        }
-    } else {  // EPI_GLU_BWD: acc = grad_inter[m, i]
-      const T* gu = (const T*)a.aux + (size_t)m * 2 * a.I;
-      T* ggu = a.out ? (T*)a.out + (size_t)m * 2 * a.I : nullptr;
-      T* gi = a.out2 ? (T*)a.out2 + (size_t)m * a.I : nullptr;
-#pragma unroll
-      for (int ti = 0; ti < C::TI; ++ti)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int i0 = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
-          if (i0 >= a.I) continue;
-          float go[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) go[j] = round_through<T>(acc[ti][tj][4 * g + j]);
-          if (gi) Store4<T>::st(gi + i0, go[0], go[1], go[2], go[3]);
-          if (ggu) {
-            float gv[4], uv[4], dg[4], du[4];
-            Store4<T>::ld(gu + i0, gv);
-            Store4<T>::ld(gu + a.I + i0, uv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              dg[j] = go[j] * uv[j] * glu_dact(code, gv[j]);
-              du[j] = go[j] * glu_act(code, gv[j]);
-            }
-            Store4<T>::st(ggu + i0, dg[0], dg[1], dg[2], dg[3]);
-            Store4<T>::st(ggu + a.I + i0, du[0], du[1], du[2], du[3]);
-          }
-        }
-    }
-  }
+  token_epilogue<C, EPI>(acc, a, e, m0, m_end, rt);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -461,6 +479,31 @@ struct WgradArgs {
   int n_rtiles, n_ctiles;
   void* out;
 };
+
+template <class C>
+__device__ __forceinline__ void wgrad_epilogue(f32x16 (&acc)[C::TI][C::TJ], const WgradArgs& a, int e,
+                                               int r0, int c0) {
+  typedef typename C::T T;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int h = lane >> 5;
+  T* outE = (T*)a.out + (size_t)e * a.C * a.R;
+#pragma unroll
+  for (int tj = 0; tj < C::TJ; ++tj) {
+    const int c = c0 + wc * C::WTC + tj * 32 + (lane & 31);
+    if (c >= a.C) continue;
+    T* o = outE + (size_t)c * a.R;
+#pragma unroll
+    for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = r0 + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+        if (r < a.R)
+          Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1], acc[ti][tj][4 * g + 2],
+                        acc[ti][tj][4 * g + 3]);
+      }
+  }
+}
 
 template <class C>
 __global__ void __launch_bounds__(C::NT)
@@ -496,25 +539,136 @@ wgrad_kernel(WgradArgs a) {
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
   mainloop<C>(acc, lp, lq, k0, k1, smem);
 
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wr = wid / C::WC, wc = wid % C::WC;
-  const int h = lane >> 5;
-  T* outE = (T*)a.out + (size_t)e * a.C * a.R;
-#pragma unroll
-  for (int tj = 0; tj < C::TJ; ++tj) {
-    const int c = c0 + wc * C::WTC + tj * 32 + (lane & 31);
-    if (c >= a.C) continue;
-    T* o = outE + (size_t)c * a.R;
-#pragma unroll
-    for (int ti = 0; ti < C::TI; ++ti)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int r = r0 + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
-        if (r < a.R)
-          Store4<T>::st(o + r, acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1], acc[ti][tj][4 * g + 2],
-                        acc[ti][tj][4 * g + 3]);
-      }
+  wgrad_epilogue<C>(acc, a, e, r0, c0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Second-generation kernels (16-bit types; 256x256 tiles, DMA-fed LDS; see moe_gemm_v2.h).
+
+template <typename T> using V2Cfg = Cfg<T, v2::TILE, v2::TILE, 2, 2>;
+
+// Physical weight row of tile row rr for the gate/up forward GEMM: in each wave's WTR rows the
+// first half are gate channels and the second half the same up channels.
+template <class C>
+__device__ __forceinline__ int glu_prow(int rr, int rt, int I, bool& ok) {
+  const int wr = rr / C::WTR, w = rr % C::WTR;
+  const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + (w % (C::WTR / 2));
+  ok = ch < I;
+  return (w >= C::WTR / 2 ? I : 0) + ch;
+}
+
+template <typename T, int EPI, bool P_RC>
+__global__ void __launch_bounds__(v2::NT, 1)
+token_gemm_v2_kernel(TokenArgs a, int n_logical) {
+  using C = V2Cfg<T>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
+  __shared__ int s_wsum[v2::NT / 64];
+
+  tile_prefix<v2::NT>(a.offsets, a.E_glu, v2::TILE, s_pref, s_wsum);
+  const int lid = v2::xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  if (lid >= n_logical) return;
+  const int mt = lid / a.n_rtiles;
+  const int rt = lid % a.n_rtiles;
+  if (mt >= s_pref[a.E_glu]) return;
+  int lo = 0, hi = a.E_glu - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
   }
+  const int e = lo;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v2::TILE;
+  const int m_end = a.offsets[e + 1];
+  const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
+
+  // Token rows past the group end read row m0 (their results are never stored).
+  v2::DmaKc lq;
+  lq.init();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int m = m0 + v2::DmaKc::row_of(i);
+    if (m >= m_end) m = m0;
+    const int qr = a.q_gather ? a.q_gather[m] : m;
+    lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
+  }
+
+  f32x16 acc[v2::TN][v2::TN];
+#pragma unroll
+  for (int ti = 0; ti < v2::TN; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < v2::TN; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+
+  if constexpr (P_RC) {
+    v2::RcReg<false> lp;
+    const int r0 = rt * v2::TILE;
+    lp.src = (const char*)(Pe + r0);
+    lp.ld = (size_t)a.p_ld * sizeof(T);
+    lp.gather = nullptr;
+    lp.kend = a.K;
+    lp.init(a.R - r0);
+    v2::mainloop<T>(acc, lp, lq, 0, a.K, smem);
+  } else {
+    v2::DmaKc lp;
+    lp.init();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = v2::DmaKc::row_of(i);
+      bool ok;
+      int prow;
+      if (EPI == EPI_GLU_FWD) {
+        prow = glu_prow<C>(rr, rt, a.I, ok);
+      } else {
+        prow = rt * v2::TILE + rr;
+        ok = prow < a.R;
+      }
+      lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+    }
+    v2::mainloop<T>(acc, lp, lq, 0, a.K, smem);
+  }
+  token_epilogue<C, EPI>(acc, a, e, m0, m_end, rt);
+}
+
+template <typename T, bool RG, bool CG>
+__global__ void __launch_bounds__(v2::NT, 1)
+wgrad_v2_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
+  using C = V2Cfg<T>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
+  // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
+  const int lid = (int)blockIdx.x;
+  if (lid >= n_logical) return;
+  const int per_e = a.n_rtiles * a.n_ctiles;
+  const int ei = lid / per_e, rem = lid % per_e;
+  const int e = order ? order[ei] : ei;
+  if (e < 0 || e >= E_glu) return;  // weightless special expert
+  const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
+  const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
+  const int r0 = rt * v2::TILE, c0 = ct * v2::TILE;
+
+  v2::RcReg<RG> lp;
+  lp.src = (const char*)((const T*)a.rsrc + r0);
+  lp.ld = (size_t)a.r_ld * sizeof(T);
+  lp.gather = a.r_gather;
+  lp.kend = k1;
+  lp.init(a.R - r0);
+  v2::RcReg<CG> lq;
+  lq.src = (const char*)((const T*)a.csrc + c0);
+  lq.ld = (size_t)a.c_ld * sizeof(T);
+  lq.gather = a.c_gather;
+  lq.kend = k1;
+  lq.init(a.C - c0);
+
+  f32x16 acc[v2::TN][v2::TN];
+#pragma unroll
+  for (int ti = 0; ti < v2::TN; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < v2::TN; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  v2::mainloop<T>(acc, lp, lq, k0, k1, smem);
+  wgrad_epilogue<C>(acc, a, e, r0, c0);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -530,7 +684,7 @@ static int launch_token(const TokenArgs& a, int64_t n_rows, hipStream_t s) {
   if (grid <= 0 || n_rows == 0) return MOE_OK;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   auto kern = token_gemm_kernel<C, EPI, P_RC>;
-  hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, s, a);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
@@ -541,8 +695,41 @@ static int launch_wgrad(const WgradArgs& a, int E, hipStream_t s) {
   if (grid <= 0) return MOE_OK;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   auto kern = wgrad_kernel<C>;
-  hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NT), C::LDS_BYTES, s, a);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+
+template <typename T, int EPI, bool P_RC>
+static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
+  a.n_rtiles = EPI == EPI_GLU_FWD ? (int)((a.I + v2::TILE / 2 - 1) / (v2::TILE / 2))
+                                  : (int)((a.R + v2::TILE - 1) / v2::TILE);
+  const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
+  const int64_t logical = max_mt * a.n_rtiles;
+  if (logical <= 0 || n_rows == 0) return MOE_OK;
+  const int64_t grid = (logical + 7) / 8 * 8;
+  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  auto kern = token_gemm_v2_kernel<T, EPI, P_RC>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+// n_entries = length of `order` (every expert id, GLU or special) or E_glu without an order.
+template <typename T>
+static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int E_glu, hipStream_t s) {
+  a.n_rtiles = (a.R + v2::TILE - 1) / v2::TILE;
+  a.n_ctiles = (a.C + v2::TILE - 1) / v2::TILE;
+  const int64_t logical = (int64_t)n_entries * a.n_rtiles * a.n_ctiles;
+  if (logical <= 0) return MOE_OK;
+  const int64_t grid = (logical + 7) / 8 * 8;
+  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  auto kern = a.r_gather ? (a.c_gather ? wgrad_v2_kernel<T, true, true> : wgrad_v2_kernel<T, true, false>)
+                         : (a.c_gather ? wgrad_v2_kernel<T, false, true> : wgrad_v2_kernel<T, false, false>);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, order, E_glu,
+                     (int)logical);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -591,6 +778,9 @@ extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int6
   a.out = gate_up_out; a.out_ld = 2 * I; a.out2 = inter_out;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_GLU_FWD, false>(a, n_rows, s);
+    }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((I + C::BR / 2 - 1) / (C::BR / 2));
     return launch_token<C, EPI_GLU_FWD, false>(a, n_rows, s);
@@ -619,6 +809,9 @@ extern "C" int moe_grouped_down_fwd(int dtype, const void* inter, const void* do
   a.out = eo_out; a.out_ld = H;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_STORE, false>(a, n_rows, s);
+    }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((H + C::BR - 1) / C::BR);
     return launch_token<C, EPI_STORE, false>(a, n_rows, s);
@@ -653,6 +846,9 @@ extern "C" int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo,
   a.out = ggu_out; a.out2 = grad_inter_out; a.aux = gate_up;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_GLU_BWD, true>(a, n_rows, s);
+    }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((I + C::BR - 1) / C::BR);
     return launch_token<C, EPI_GLU_BWD, true>(a, n_rows, s);
@@ -682,6 +878,9 @@ extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gat
   a.out = grad_xs_out; a.out_ld = H;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_STORE, true>(a, n_rows, s);
+    }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((H + C::BR - 1) / C::BR);
     return launch_token<C, EPI_STORE, true>(a, n_rows, s);
@@ -695,12 +894,14 @@ extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gat
 
 extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
                                  const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R,
-                                 int64_t C, const int32_t* offsets, int E_glu, void* out,
-                                 void* stream) {
+                                 int64_t C, const int32_t* offsets, const int32_t* expert_order,
+                                 int n_experts, int E_glu, void* out, void* stream) {
   if (dtype != MOE_DT_F32 && dtype != MOE_DT_F16 && dtype != MOE_DT_BF16) return MOE_ERR_DTYPE;
-  if (R <= 0 || C <= 0 || E_glu <= 0 || R >= (1 << 30) || C >= (1 << 30)) return MOE_ERR_SHAPE;
+  if (R <= 0 || C <= 0 || E_glu <= 0 || E_glu > MAX_GLU_EXPERTS || R >= (1 << 30) || C >= (1 << 30))
+    return MOE_ERR_SHAPE;
+  if (expert_order && (n_experts < E_glu || n_experts > MAX_GLU_EXPERTS)) return MOE_ERR_SHAPE;
   if (!rsrc || !csrc || !offsets || !out) return MOE_ERR_SHAPE;
-  if (R % 8 != 0 || r_ld % 8 != 0 || c_ld % 8 != 0 || C % 4 != 0) return MOE_ERR_ALIGN;
+  if (R % 8 != 0 || C % 8 != 0 || r_ld % 8 != 0 || c_ld % 8 != 0) return MOE_ERR_ALIGN;
   if (!aligned16(rsrc) || !aligned16(csrc) || !aligned16(out)) return MOE_ERR_ALIGN;
   WgradArgs a = {};
   a.rsrc = rsrc; a.r_ld = r_ld; a.r_gather = r_gather;
@@ -708,6 +909,9 @@ extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, cons
   a.R = (int)R; a.C = (int)C; a.offsets = offsets; a.out = out;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
+    if constexpr (sizeof(T) == 2) {
+      return launch_wgrad_v2<T>(a, expert_order, expert_order ? n_experts : E_glu, E_glu, s);
+    }
     using Cc = WgCfg<T>;
     a.n_rtiles = (int)((R + Cc::BR - 1) / Cc::BR);
     a.n_ctiles = (int)((C + Cc::BC - 1) / Cc::BC);

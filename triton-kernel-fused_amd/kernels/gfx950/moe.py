@@ -104,6 +104,8 @@ class _Routing:
         self.counts = torch.empty(n_experts, **i32)
         self.offsets = torch.empty(n_experts + 1, **i32)
         self.tile_offsets = torch.empty(n_experts + 1, **i32)
+        self.expert_order = torch.empty(n_experts, **i32)
+        self.n_experts = n_experts
         self.sorted_token = torch.empty(max(m, 1), **i32)
         self.sorted_flat = torch.empty(max(m, 1), **i32)
         self.flat_to_sorted = torch.empty(max(m, 1), **i32)
@@ -111,7 +113,8 @@ class _Routing:
         ws = _lib.lib().moe_get_workspace_size(n, k, n_experts)
         self.workspace = torch.empty(max(ws, 256), device=dev, dtype=torch.uint8)
         _lib.call("moe_dispatch", _lib.ptr(idx), n, k, n_experts, _lib.ptr(self.counts),
-                  _lib.ptr(self.offsets), _lib.ptr(self.tile_offsets), _lib.ptr(self.sorted_token),
+                  _lib.ptr(self.offsets), _lib.ptr(self.tile_offsets), _lib.ptr(self.expert_order),
+                  _lib.ptr(self.sorted_token),
                   _lib.ptr(self.sorted_flat), _lib.ptr(self.flat_to_sorted), _lib.ptr(self.status),
                   _lib.ptr(self.workspace), self.workspace.numel(), _lib.stream_of(dev))
         if _CHECK_INDICES and int(self.status.item()) != 0:
@@ -264,12 +267,14 @@ class _MoEFunction(torch.autograd.Function):
                 g_dw = torch.empty_like(down_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(inter), inter_dim, None,
                           _lib.ptr(grad_eo), h, None, inter_dim, h, _lib.ptr(routing.offsets),
-                          e_glu, _lib.ptr(g_dw), stream, tag="down")
+                          _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw), stream,
+                          tag="down")
             if need_gu:
                 g_gu = torch.empty_like(gate_up_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(hidden), h,
                           _lib.ptr(routing.sorted_token), _lib.ptr(ggu), two_i, None, h, two_i,
-                          _lib.ptr(routing.offsets), e_glu, _lib.ptr(g_gu), stream, tag="gate_up")
+                          _lib.ptr(routing.offsets), _lib.ptr(routing.expert_order), n_exp, e_glu,
+                          _lib.ptr(g_gu), stream, tag="gate_up")
         elif e_glu > 0:
             if need_dw:
                 g_dw = torch.zeros_like(down_proj)
