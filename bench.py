@@ -100,6 +100,74 @@ def run_bf16(config, steps, warmup, timer=True):
     return dict(cfg=cfg, ms=ms, tflops=f / (ms * 1e-3) / 1e12, kernels=kern, mhi=mhi)
 
 
+def _timed(fn, steps, warmup, timer=True):
+    import torch
+    from kernels import _lib
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    records = []
+    if timer:
+        _lib.set_timer(records)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.set_timer(None)
+    per = {}
+    for name, e0, e1 in records:
+        per.setdefault(name, []).append(e0.elapsed_time(e1))
+    return (t1 - t0) * 1e3 / steps, {k: statistics.mean(v) for k, v in per.items()}
+
+
+def run_fp8(steps, warmup):
+    """Config 4: fp8 forward; FLOPs 6*M*H*I over the routed rows."""
+    import kernels
+    from kernels.workloads import make_workload, flops
+    w = make_workload(4, device="cuda", seed=0)
+    cfg = w["cfg"]
+    args = (w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"],
+            w["down_q"], w["down_scale"])
+    ms, kern = _timed(lambda: kernels.moe_fp8(*args), steps, warmup)
+    f = flops(cfg, backward=False)
+    call = kern.get("moe_fp8_fwd")
+    return {"tflops": round(f / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 4),
+            "frac_of_peak": round(f / (ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "gemm_call_ms": round(call, 4) if call else None,
+            "gemm_call_tflops": round(f / (call * 1e-3) / 1e12, 1) if call else None,
+            "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
+            "workload": (f"{cfg['name']}: fp8-e4m3 fwd N={cfg['N']} H={cfg['H']} I={cfg['I']} "
+                         f"E={cfg['E']} k={cfg['k']}, peak {PEAK_FP8_TFLOPS} TFLOP/s")}
+
+
+def run_mxfp8(steps, warmup):
+    """Config 5: MXFP8-weight decode forward; algorithmic bytes = every touched expert's weights
+    (e4m3 + one E8M0 byte per 32) + x read + out written + routing metadata."""
+    import torch
+    import kernels
+    from kernels.workloads import make_workload
+    w = make_workload(5, device="cuda", seed=0)
+    cfg = w["cfg"]
+    n, h, i, k = cfg["N"], cfg["H"], cfg["I"], cfg["k"]
+    touched = int(torch.unique(w["idx"]).numel())
+    weight_bytes = touched * 3 * h * i * (1 + 1 / 32)
+    io_bytes = 2 * n * h * 2 + n * k * (8 + 2)
+    args = (w["hidden"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"], w["down_q"],
+            w["down_scale"])
+    ms, kern = _timed(lambda: kernels.moe_mxfp8(*args), steps, warmup)
+    gbs = (weight_bytes + io_bytes) / (ms * 1e-3) / 1e9
+    call = kern.get("moe_mxfp8_fwd")
+    return {"gbs": round(gbs, 1), "ms_per_step": round(ms, 4),
+            "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "touched_experts": touched,
+            "algorithmic_bytes": int(weight_bytes + io_bytes),
+            "gemm_call_ms": round(call, 4) if call else None,
+            "gemm_call_gbs": round(weight_bytes / (call * 1e-3) / 1e9, 1) if call else None,
+            "kernels_ms": {k2: round(v, 4) for k2, v in kern.items()},
+            "workload": (f"{cfg['name']}: MXFP8 weights, bf16 activations, fwd N={n} H={h} I={i} "
+                         f"E={cfg['E']} k={k}, peak {PEAK_HBM_GBS} GB/s")}
+
+
 def cpu_baseline(config, sample_tokens, reps=3):
     """The oracle's fp32 eager MoE fwd+bwd (a restatement of the reference moe_eager, PyTorch on
     the host cores), on the first `sample_tokens` tokens of the same workload."""
@@ -139,6 +207,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="for rocprofv3 --pmc runs: 1 warmup + 1 step of the workload, then a plain "
+                         "1 GiB device copy whose counters calibrate the traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (all experts resident, "
@@ -149,6 +220,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs the GPU", file=sys.stderr)
         sys.exit(1)
+
+    if args.profile_pass:
+        run_bf16(args.config, 1, 1, timer=False)
+        src = torch.empty(1 << 29, device="cuda", dtype=torch.bfloat16).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)             # the calibration kernel: reads 1 GiB, writes 1 GiB
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_pass": args.config, "calibration_copy_bytes": 1 << 30}))
+        return
 
     _log(f"config {args.config}: warmup {args.warmup}, steps {args.steps}")
     r = run_bf16(args.config, args.steps, args.warmup)
@@ -180,6 +261,10 @@ def main():
         line["extra_configs"] = {r2["cfg"]["name"]: {"tflops": round(r2["tflops"], 2),
                                                      "ms_per_step": round(r2["ms"], 4),
                                                      "frac_of_peak": round(r2["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+        _log("extra config 4 (fp8 fwd)")
+        line["extra_configs"]["fp8_fwd"] = run_fp8(max(5, args.steps // 2), 2)
+        _log("extra config 5 (MXFP8 decode)")
+        line["extra_configs"]["mxfp8_decode"] = run_mxfp8(max(10, args.steps), 3)
     if not args.no_cpu:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)

@@ -159,6 +159,33 @@ int moe_glu_bwd(int dtype, const void* grad_out, int64_t go_row_stride, int64_t 
                 const float* gamma, int ap_stride, int64_t n_rows, int64_t I, void* ggu_out,
                 int64_t ggu_ld, float* da_out, float* dg_out, void* stream);
 
+/* fp8-e4m3 forward (inference; BASELINE config 4; no counterpart in the reference, which has no
+ * fp8 path — the algorithm is the bf16 pipeline of moe_grouped_gateup_swiglu_fwd /
+ * moe_grouped_down_fwd with quantised operands). x_q (N,H) e4m3 + x_scale (N) fp32 (per token);
+ * w13_q (E,2I,H) e4m3 + w13_scale (E,2I) fp32 and w2_q (E,H,I) + w2_scale (E,H) fp32 (per
+ * output channel). Writes inter (M,I) bf16 = SiLU(gate)*up, inter_q (M,I) e4m3 + inter_scale (M)
+ * (per routed row, absmax/448) and eo (M,H) bf16; moe_combine_fwd (bf16) makes the output.
+ * H and I must be multiples of 128. */
+int moe_fp8_fwd(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t H,
+                const void* w13_q, const float* w13_scale, const void* w2_q, const float* w2_scale,
+                int E, int64_t I, const int32_t* offsets, const int32_t* sorted_token,
+                int64_t n_rows, void* inter, void* inter_q, float* inter_scale, void* eo,
+                void* stream);
+
+/* Per-row absmax fp8 quantisation: scale[m] = absmax(x[m,:]) / 448 (1 for a zero row),
+ * q = e4m3(x / scale), round to nearest even. x (n_rows, K) bf16, K a multiple of 8. */
+int moe_rowquant_fp8(const void* x, int64_t n_rows, int64_t K, void* q, float* scale,
+                     void* stream);
+
+/* MXFP8-weight forward for decode batches (no counterpart in the reference).
+ * hidden (N,H) bf16; w13_q (E,2I,H) e4m3 + w13_scale (E,2I,H/32) E8M0 bytes; w2_q (E,H,I) e4m3 +
+ * w2_scale (E,H,I/32) E8M0 (value 2^(s-127), OCP MX). Writes inter (M,I) bf16 and eo (M,H) bf16;
+ * moe_combine_fwd (bf16) makes the output. H and I must be multiples of 512. */
+int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, const void* w13_q,
+                  const void* w13_scale, const void* w2_q, const void* w2_scale, int E, int64_t I,
+                  const int32_t* offsets, const int32_t* sorted_token, int64_t n_rows, void* inter,
+                  void* eo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

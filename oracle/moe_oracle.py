@@ -210,15 +210,16 @@ def e4m3_round(x):
 
 
 def fp8_forward(x_q, x_scale, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale,
-                requant_inter=True):
-    """fp8 MoE forward in fp32 from quantised operands (all CPU tensors).
-    gate_up = (x_q . W_q^T) * x_scale[t] * w_scale[n]; inter = SiLU(gate)*up, re-quantised per
-    row (absmax/448) when requant_inter; eo = (inter_q . Wd_q^T) * inter_scale * wd_scale[h];
+                requant_inter=True, inter_bf16=False):
+    """fp8 MoE forward in fp32 from quantised operands.
+    gate_up = (x_q . W_q^T) * x_scale[t] * w_scale[n]; inter = SiLU(gate)*up (rounded to bf16 first
+    when inter_bf16, as a kernel that stores it in bf16 does), re-quantised per row (absmax/448)
+    when requant_inter; eo = (inter_q . Wd_q^T) * inter_scale * wd_scale[h];
     out[t] = sum_j w[t,j] * eo (fp32). Returns fp32 (N,H)."""
     n, h = x_q.shape
     inter = gate_up_q.shape[1] // 2
     xf = x_q.float()
-    out = torch.zeros(n, h)
+    out = torch.zeros(n, h, device=x_q.device)
     for e in range(gate_up_q.shape[0]):
         hit = idx == e
         rows = hit.any(-1)
@@ -227,6 +228,8 @@ def fp8_forward(x_q, x_scale, idx, wt, gate_up_q, gate_up_scale, down_q, down_sc
         w = (wt.float() * hit).sum(-1)[rows].unsqueeze(-1)
         gu = (xf[rows] @ gate_up_q[e].float().T) * x_scale[rows].unsqueeze(-1) * gate_up_scale[e]
         y = F.silu(gu[:, :inter]) * gu[:, inter:]
+        if inter_bf16:
+            y = y.bfloat16().float()
         if requant_inter:
             amax = y.abs().amax(-1, keepdim=True)
             s = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
@@ -242,7 +245,7 @@ def mxfp8_forward(hidden, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale)
     n, h = hidden.shape
     inter = gate_up_q.shape[1] // 2
     x = hidden.float()
-    out = torch.zeros(n, h)
+    out = torch.zeros(n, h, device=hidden.device)
 
     def deq(q, s):
         k = q.shape[-1]

@@ -35,29 +35,43 @@ template <typename T> __device__ __forceinline__ float round_through(float v) {
   return to_f32(from_f32<T>(v));
 }
 
-// MFMA traits per element type. Each lane holds one 16-byte chunk of K per "slab": the two lane
-// halves (lanes 0-31 and 32-63) hold consecutive 16-byte chunks, so one slab spans 32 bytes of K.
-// Operand P feeds the MFMA A side (rows of the 32x32 output), operand Q the B side (columns).
+// fp8 e4m3 (OCP "fn": bias 7, max 448, no infinities) operand tag; one byte per element.
+struct fp8e4m3 { unsigned char bits; };
+
+// MFMA traits per operand element type. A lane holds CPL 16-byte chunks of K per MFMA: the two
+// lane halves (lanes 0-31 and 32-63) hold consecutive CPL-chunk runs, so one MFMA ("slab") spans
+// 32*CPL bytes of K. Only the pairing of A and B elements matters to the sum, so any K order
+// shared by both operands is valid. Operand P feeds the MFMA A side (rows of the 32x32 output),
+// operand Q the B side (columns).
 template <typename T> struct Mfma;
 
 template <> struct Mfma<bf16> {
   static constexpr int VEC = 8;  // elements per 16 bytes
+  static constexpr int CPL = 1;
   __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
+    step(c, a[0], b[0]);
   }
 };
 
 template <> struct Mfma<f16> {
   static constexpr int VEC = 8;
+  static constexpr int CPL = 1;
   __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
+    step(c, a[0], b[0]);
   }
 };
 
 template <> struct Mfma<float> {
   static constexpr int VEC = 4;
+  static constexpr int CPL = 1;
   // v_mfma_f32_32x32x2f32 consumes one fp32 per lane and K=2 per instruction (one value per lane
   // half), so a 16-byte chunk (4 consecutive K values per lane) is four instructions.
   __device__ __forceinline__ static void step(f32x16& c, i32x4 a, i32x4 b) {
@@ -66,6 +80,21 @@ template <> struct Mfma<float> {
     const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
 #pragma unroll
     for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(af[j], bf[j], c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
+    step(c, a[0], b[0]);
+  }
+};
+
+// fp8 x fp8 on the gfx950 f8f6f4 MFMA (32x32x64, 32 e4m3 bytes per lane). The scaled form with
+// both E8M0 scales = 127 (2^0) is the unscaled product; format code 0 = fp8 e4m3 for A and B.
+template <> struct Mfma<fp8e4m3> {
+  static constexpr int VEC = 16;
+  static constexpr int CPL = 2;
+  __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
+    const i32x8 a8 = __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const i32x8 b8 = __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 0, 0, 0, 127, 0, 127);
   }
 };
 

@@ -1,0 +1,244 @@
+// fp8-e4m3 MoE forward (inference): grouped gate/up GEMM with scales + SwiGLU, per-row
+// re-quantisation of the intermediate, grouped down GEMM with scales.
+//
+// Operands are OCP e4m3fn with fp32 scales: activations per token, weights per output channel,
+// the intermediate per routed row (absmax / 448). The GEMMs run the 256x256 DMA-fed pipeline of
+// moe_gemm_v2.h on v_mfma_scale_f32_32x32x64_f8f6f4 with neutral E8M0 scales (the plain fp8
+// product); the per-token and per-channel scales factor out of the K sum and are applied in the
+// epilogue: y[m, n] = (sum_k xq[m,k] wq[n,k]) * sx[m] * sw[n].
+// The gate/up epilogue cannot quantise the intermediate itself (a row's absmax spans every
+// column tile), so it stores SiLU(gate)*up in bf16 and a row kernel quantises it.
+#include "moe_gemm_common.h"
+#include "moe_gemm_v2.h"
+
+namespace moe {
+
+struct Fp8Args {
+  const fp8e4m3* P;        // weight rows, K contiguous
+  long long p_e, p_ld;     // elements between experts / rows
+  const float* p_scale;    // per (expert, weight row) fp32 scales
+  long long ps_e;          // scales between experts
+  int R, K, I;
+  const fp8e4m3* Q;        // token-side rows, K contiguous
+  long long q_ld;
+  const int32_t* q_gather; // sorted row -> Q row, or null
+  const float* q_scale;    // per Q row (indexed like Q rows)
+  const int32_t* offsets;
+  int E_glu, n_rtiles;
+  bf16* out;               // GLU: inter (M, I); plain: (M, out_ld)
+  long long out_ld;
+};
+
+template <bool GLU>
+__global__ void __launch_bounds__(v2::NT, 1)
+fp8_gemm_kernel(Fp8Args a, int n_logical) {
+  using C = Cfg<fp8e4m3, v2::TILE, v2::TILE, 2, 2>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
+  __shared__ int s_wsum[v2::NT / 64];
+
+  tile_prefix<v2::NT>(a.offsets, a.E_glu, v2::TILE, s_pref, s_wsum);
+  const int lid = v2::xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  if (lid >= n_logical) return;
+  const int mt = lid / a.n_rtiles;
+  const int rt = lid % a.n_rtiles;
+  if (mt >= s_pref[a.E_glu]) return;
+  int lo = 0, hi = a.E_glu - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
+  }
+  const int e = lo;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v2::TILE;
+  const int m_end = a.offsets[e + 1];
+  const fp8e4m3* Pe = a.P + (size_t)e * a.p_e;
+
+  v2::DmaKc lq;
+  lq.init();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int m = m0 + v2::DmaKc::row_of(i);
+    if (m >= m_end) m = m0;
+    const int qr = a.q_gather ? a.q_gather[m] : m;
+    lq.rowp[i] = (const char*)(a.Q + (size_t)qr * a.q_ld);
+  }
+  v2::DmaKc lp;
+  lp.init();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int rr = v2::DmaKc::row_of(i);
+    bool ok;
+    int prow;
+    if (GLU) {
+      prow = glu_prow<C>(rr, rt, a.I, ok);
+    } else {
+      prow = rt * v2::TILE + rr;
+      ok = prow < a.R;
+    }
+    lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+  }
+
+  f32x16 acc[v2::TN][v2::TN];
+#pragma unroll
+  for (int ti = 0; ti < v2::TN; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < v2::TN; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  v2::mainloop<fp8e4m3>(acc, lp, lq, 0, a.K, smem);
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wr = wid / C::WC, wc = wid % C::WC;
+  const int h = lane >> 5;
+  const float* ps = a.p_scale + (size_t)e * a.ps_e;
+  static_for<0, C::TJ>([&](auto tj_c) {
+    constexpr int tj = decltype(tj_c)::value;
+    const int m = m0 + wc * C::WTC + tj * 32 + (lane & 31);
+    if (m >= m_end) return;
+    const float qs = a.q_scale[a.q_gather ? a.q_gather[m] : m];
+    if constexpr (GLU) {
+      bf16* it = a.out + (size_t)m * a.I;
+#pragma unroll
+      for (int ti = 0; ti < C::TI / 2; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + ti * 32 + 8 * g + 4 * h;
+          if (ch >= a.I) continue;
+          const f32x4 sg = *(const f32x4*)(ps + ch);
+          const f32x4 su = *(const f32x4*)(ps + a.I + ch);
+          float iv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float gv = acc[ti][tj][4 * g + j] * qs * sg[j];
+            const float uv = acc[ti + C::TI / 2][tj][4 * g + j] * qs * su[j];
+            iv[j] = silu(gv) * uv;
+          }
+          Store4<bf16>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
+        }
+    } else {
+      bf16* o = a.out + (size_t)m * a.out_ld;
+#pragma unroll
+      for (int ti = 0; ti < C::TI; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+          if (r >= a.R) continue;
+          const f32x4 sr = *(const f32x4*)(ps + r);
+          Store4<bf16>::st(o + r, acc[ti][tj][4 * g] * qs * sr[0], acc[ti][tj][4 * g + 1] * qs * sr[1],
+                           acc[ti][tj][4 * g + 2] * qs * sr[2], acc[ti][tj][4 * g + 3] * qs * sr[3]);
+        }
+    }
+  });
+}
+
+// Per-row absmax fp8 quantisation of a bf16 matrix (one wave per row):
+// scale[m] = absmax(row) / 448 (1 for an all-zero row), q[m, :] = e4m3(x / scale).
+__global__ void __launch_bounds__(256)
+rowquant_fp8_kernel(const bf16* __restrict__ x, int64_t M, int K, fp8e4m3* __restrict__ q,
+                    float* __restrict__ scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const bf16* xr = x + row * K;
+  float amax = 0.f;
+  for (int c = lane * 8; c < K; c += 512) {
+    const uint4 u = *(const uint4*)(xr + c);
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(w[i] << 16)),
+                               fabsf(__uint_as_float(w[i] & 0xffff0000u))));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 64));
+  const float s = amax > 0.f ? amax / 448.f : 1.f;
+  if (lane == 0) scale[row] = s;
+  fp8e4m3* qr = q + row * K;
+  for (int c = lane * 8; c < K; c += 512) {
+    const uint4 u = *(const uint4*)(xr + c);
+    const unsigned w[4] = {u.x, u.y, u.z, u.w};
+    int packed[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float v0 = __uint_as_float(w[2 * i] << 16) / s;
+      const float v1 = __uint_as_float(w[2 * i] & 0xffff0000u) / s;
+      const float v2 = __uint_as_float(w[2 * i + 1] << 16) / s;
+      const float v3 = __uint_as_float(w[2 * i + 1] & 0xffff0000u) / s;
+      int p = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+      p = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, p, true);
+      packed[i] = p;
+    }
+    *(uint2*)(qr + c) = uint2{(unsigned)packed[0], (unsigned)packed[1]};
+  }
+}
+
+template <bool GLU>
+static int launch_fp8(Fp8Args a, int64_t n_rows, hipStream_t s) {
+  a.n_rtiles = GLU ? (a.I + v2::TILE / 2 - 1) / (v2::TILE / 2) : (a.R + v2::TILE - 1) / v2::TILE;
+  const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
+  const int64_t logical = max_mt * a.n_rtiles;
+  if (logical <= 0) return MOE_OK;
+  const int64_t grid = (logical + 7) / 8 * 8;
+  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  auto kern = fp8_gemm_kernel<GLU>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int moe_fp8_fwd(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t H,
+                           const void* w13_q, const float* w13_scale, const void* w2_q,
+                           const float* w2_scale, int E, int64_t I, const int32_t* offsets,
+                           const int32_t* sorted_token, int64_t n_rows, void* inter,
+                           void* inter_q, float* inter_scale, void* eo, void* stream) {
+  if (n_tokens < 0 || H <= 0 || I <= 0 || E <= 0 || E > MAX_GLU_EXPERTS || n_rows < 0)
+    return MOE_ERR_SHAPE;
+  if (H >= (1 << 30) || I >= (1 << 29) || n_rows >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
+  if (H % 128 != 0 || I % 128 != 0) return MOE_ERR_ALIGN;
+  if (n_rows == 0) return MOE_OK;
+  if (!x_q || !x_scale || !w13_q || !w13_scale || !w2_q || !w2_scale || !offsets ||
+      !sorted_token || !inter || !inter_q || !inter_scale || !eo)
+    return MOE_ERR_SHAPE;
+  if (!al16(x_q) || !al16(w13_q) || !al16(w2_q) || !al16(w13_scale) || !al16(w2_scale) ||
+      !al16(inter) || !al16(inter_q) || !al16(eo))
+    return MOE_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  Fp8Args g = {};
+  g.P = (const fp8e4m3*)w13_q; g.p_e = 2 * I * H; g.p_ld = H;
+  g.p_scale = w13_scale; g.ps_e = 2 * I;
+  g.R = (int)(2 * I); g.K = (int)H; g.I = (int)I;
+  g.Q = (const fp8e4m3*)x_q; g.q_ld = H; g.q_gather = sorted_token; g.q_scale = x_scale;
+  g.offsets = offsets; g.E_glu = E;
+  g.out = (bf16*)inter; g.out_ld = I;
+  int st = launch_fp8<true>(g, n_rows, s);
+  if (st) return st;
+  hipLaunchKernelGGL(rowquant_fp8_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, s,
+                     (const bf16*)inter, n_rows, (int)I, (fp8e4m3*)inter_q, inter_scale);
+  if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+  Fp8Args d = {};
+  d.P = (const fp8e4m3*)w2_q; d.p_e = H * I; d.p_ld = I;
+  d.p_scale = w2_scale; d.ps_e = H;
+  d.R = (int)H; d.K = (int)I; d.I = (int)I;
+  d.Q = (const fp8e4m3*)inter_q; d.q_ld = I; d.q_gather = nullptr; d.q_scale = inter_scale;
+  d.offsets = offsets; d.E_glu = E;
+  d.out = (bf16*)eo; d.out_ld = H;
+  return launch_fp8<false>(d, n_rows, s);
+}
+
+extern "C" int moe_rowquant_fp8(const void* x, int64_t n_rows, int64_t K, void* q, float* scale,
+                                void* stream) {
+  if (n_rows < 0 || K <= 0 || K >= (1 << 30)) return MOE_ERR_SHAPE;
+  if (K % 8 != 0) return MOE_ERR_ALIGN;
+  if (n_rows == 0) return MOE_OK;
+  if (!x || !q || !scale) return MOE_ERR_SHAPE;
+  if (!al16(x) || ((uintptr_t)q & 7)) return MOE_ERR_ALIGN;
+  hipLaunchKernelGGL(rowquant_fp8_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const bf16*)x, n_rows, (int)K, (fp8e4m3*)q, scale);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}

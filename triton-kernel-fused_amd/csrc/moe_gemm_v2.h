@@ -3,10 +3,12 @@
 // 64 elements double-buffered in 128 KB of LDS.
 //
 // LDS layout: each operand tile is 256 rows x 128 bytes (one K step), unpadded, with the 16-byte
-// chunk index XOR-ed by (row & 7). That makes the MFMA operand reads (32 consecutive rows, one
-// 16-byte chunk each) and the transposing stores bank-conflict-free, and it lets a wave fill 8
-// whole rows with one direct-to-LDS load (global_load_lds_dwordx4: lane l writes bytes
-// [16l, 16l+16) of a 1 KB block; the lane loads the global chunk that belongs in that slot).
+// chunk index XOR-ed by ((row >> 1) & 7). A row is half of the 64 four-byte banks, so even and
+// odd rows use different halves and the XOR spreads 8 rows of each parity over all chunks: the
+// MFMA operand reads (16 consecutive rows per 256-byte LDS cycle, one 16-byte chunk each) are
+// conflict-free. A wave fills 8 whole rows with one direct-to-LDS load (global_load_lds_dwordx4:
+// lane l writes bytes [16l, 16l+16) of a 1 KB block; the lane loads the global chunk that belongs
+// in that slot).
 //
 // K-contiguous operands (activations, weights in the forward) go global->LDS by DMA without
 // touching registers. Row-contiguous operands (weights in the dX GEMMs, both wgrad operands) are
@@ -26,27 +28,29 @@ constexpr int NT = 256;
 constexpr int TILE = 256;        // rows of each operand tile (P and Q)
 constexpr int WT = 128;          // rows of a wave's sub-tile
 constexpr int TN = WT / 32;      // MFMA tiles per wave side (4)
-constexpr int ROWB = 128;        // bytes per LDS row = one K step of 64 16-bit values
-constexpr int BK = 64;
+constexpr int ROWB = 128;        // bytes per LDS row = one K step (64 16-bit or 128 fp8 values)
+constexpr int BK = 64;           // K elements per step for 16-bit operands
+template <typename T> constexpr int bk() { return ROWB / (int)sizeof(T); }
 constexpr int OPB = TILE * ROWB; // 32 KB per operand per stage
 constexpr int STAGEB = 2 * OPB;
 constexpr int LDSB = 2 * STAGEB; // 128 KB
 
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return row * ROWB + ((chunk ^ (row & 7)) << 4);
+  return row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// K-contiguous operand loaded by DMA. Lane l of wave w fills tile rows w*64 + i*8 + l/8 (i < 8),
-// physical chunk l%8, i.e. logical chunk (l%8) ^ (l/8).
+// K-contiguous operand loaded by DMA. Lane l of wave w fills tile row R = w*64 + i*8 + l/8 (i < 8),
+// physical chunk l%8, i.e. logical chunk (l%8) ^ ((R >> 1) & 7) = (l%8) ^ ((4*(i&1) + l/16) & 7).
 struct DmaKc {
   const char* rowp[8];  // global start of this lane's 8 rows (clamped to a valid row if unused)
-  int cbyte;
+  int cbyte[2];         // byte offset of this lane's logical chunk for even / odd i
 
   __device__ __forceinline__ void init() {
     const int lane = threadIdx.x & 63;
-    cbyte = ((lane & 7) ^ (lane >> 3)) << 4;
+    cbyte[0] = ((lane & 7) ^ (lane >> 4)) << 4;
+    cbyte[1] = ((lane & 7) ^ ((4 + (lane >> 4)) & 7)) << 4;
   }
   __device__ __forceinline__ static int row_of(int i) {
     return (int)(threadIdx.x >> 6) * 64 + i * 8 + (int)((threadIdx.x & 63) >> 3);
@@ -54,11 +58,11 @@ struct DmaKc {
   template <typename T>
   __device__ __forceinline__ void issue(char* op, int k) {
     char* base = op + (int)(threadIdx.x >> 6) * 64 * ROWB;
-    const int kb = k * (int)sizeof(T) + cbyte;
+    const int kb = k * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      __builtin_amdgcn_global_load_lds((glb_void*)(rowp[i] + kb), (lds_void*)(base + i * 8 * ROWB),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_void*)(rowp[i] + kb + cbyte[i & 1]),
+                                       (lds_void*)(base + i * 8 * ROWB), 16, 0, 0);
   }
   __device__ __forceinline__ void prime(int) {}
   __device__ __forceinline__ void commit(char*) const {}
@@ -125,18 +129,22 @@ struct RcReg {
   }
 };
 
-// acc[ti][tj] += P(wave rows) . Q(wave cols) over K in [k0, k1).
+// acc[ti][tj] += P(wave rows) . Q(wave cols) over K in [k0, k1). T is the operand element type;
+// a K step is ROWB bytes, i.e. SLABS MFMAs of 2*CPL 16-byte chunks each.
 template <typename T, class LP, class LQ>
 __device__ __forceinline__ void mainloop(f32x16 (&acc)[TN][TN], LP& lp, LQ& lq, int k0, int k1,
                                          char* smem) {
-  const int nk = (k1 - k0 + BK - 1) / BK;
+  constexpr int KS = bk<T>();
+  constexpr int CPL = Mfma<T>::CPL;
+  constexpr int SLABS = ROWB / (32 * CPL);
+  const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int wr = w >> 1, wc = w & 1;
   const int pbase = (wr * WT + (lane & 31)) * ROWB;
   const int qbase = OPB + (wc * WT + (lane & 31)) * ROWB;
-  const int half = lane >> 5, sw = lane & 7;
+  const int half = lane >> 5, sw = (lane >> 1) & 7;  // rows wbase + t*32 + (lane&31)
 
   lp.prime(k0);
   lq.prime(k0);
@@ -151,21 +159,33 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[TN][TN], LP& lp, LQ& lq, 
     char* nxt = smem + ((it + 1) & 1) * STAGEB;
     const bool more = it + 1 < nk;
     if (more) {
-      lp.template issue<T>(nxt, k0 + (it + 1) * BK);
-      lq.template issue<T>(nxt + OPB, k0 + (it + 1) * BK);
+      lp.template issue<T>(nxt, k0 + (it + 1) * KS);
+      lq.template issue<T>(nxt + OPB, k0 + (it + 1) * KS);
     }
+    // Operand fragments are double-buffered in registers: slab s+1 is read from LDS while the 16
+    // MFMAs of slab s execute.
+    i32x4 a[2][TN][CPL], b[2][TN][CPL];
+    auto load = [&](int f, int s) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int cb = ((2 * s + half) ^ sw) << 4;
-      i32x4 a[TN], b[TN];
+      for (int c = 0; c < CPL; ++c) {
+        const int cb = (((2 * s + half) * CPL + c) ^ sw) << 4;
 #pragma unroll
-      for (int t = 0; t < TN; ++t) a[t] = *(const i32x4*)(cur + pbase + t * 32 * ROWB + cb);
+        for (int t = 0; t < TN; ++t) a[f][t][c] = *(const i32x4*)(cur + pbase + t * 32 * ROWB + cb);
 #pragma unroll
-      for (int t = 0; t < TN; ++t) b[t] = *(const i32x4*)(cur + qbase + t * 32 * ROWB + cb);
+        for (int t = 0; t < TN; ++t) b[f][t][c] = *(const i32x4*)(cur + qbase + t * 32 * ROWB + cb);
+      }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int s = 0; s < SLABS; ++s) {
+      const int f = s & 1;
+      if (s + 1 < SLABS) load(f ^ 1, s + 1);
+      // Keep the prefetch above the MFMAs (the scheduler would otherwise sink each read to its use).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int ti = 0; ti < TN; ++ti)
 #pragma unroll
-        for (int tj = 0; tj < TN; ++tj) Mfma<T>::step(acc[ti][tj], a[ti], b[tj]);
+        for (int tj = 0; tj < TN; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
     }
     if (more) {
       lp.commit(nxt);

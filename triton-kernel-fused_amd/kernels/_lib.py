@@ -36,6 +36,9 @@ _SIGS = {
     "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_glu_fwd": [_I, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P],
     "moe_glu_bwd": [_I, _P, _L, _L, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P],
+    "moe_fp8_fwd": [_P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P, _P, _P],
+    "moe_rowquant_fp8": [_P, _L, _L, _P, _P, _P],
+    "moe_mxfp8_fwd": [_P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P],
 }
 _RESTYPES = {"moe_version": ctypes.c_char_p, "moe_get_workspace_size": ctypes.c_size_t}
 
