@@ -222,7 +222,12 @@ def main():
         sys.exit(1)
 
     if args.profile_pass:
-        run_bf16(args.config, 1, 1, timer=False)
+        if args.config == 4:
+            run_fp8(1, 1)
+        elif args.config == 5:
+            run_mxfp8(1, 1)
+        else:
+            run_bf16(args.config, 1, 1, timer=False)
         src = torch.empty(1 << 29, device="cuda", dtype=torch.bfloat16).fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
