@@ -46,16 +46,22 @@ __device__ __forceinline__ i32x4 dequant8(unsigned lo, unsigned hi, float sc) {
                __builtin_bit_cast(int, d)};
 }
 
-template <bool GLU>
-__global__ void __launch_bounds__(256)
+// KSPLIT waves share one row tile and split its K range (partials summed through LDS); the
+// block's 4/KSPLIT tiles are consecutive row tiles. a.n_rtiles counts row tiles.
+template <bool GLU, int KSPLIT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
-  const int e = (int)blockIdx.x / a.n_rtiles;
-  const int rt = (int)blockIdx.x % a.n_rtiles;
+  constexpr int TPB = 4 / KSPLIT;  // row tiles per block
+  const int nb = (a.n_rtiles + TPB - 1) / TPB;
+  const int e = (int)blockIdx.x / nb;
   const int m_begin = a.offsets[e], m_end = a.offsets[e + 1];
   if (m_begin >= m_end) return;
-  __shared__ f32x16 red[3][2][64];  // partial accumulators of waves 1..3
+  __shared__ f32x16 red[4][2][64];  // partial accumulators
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int w = wv % KSPLIT;                                      // K part of this wave
+  const int rt = ((int)blockIdx.x % nb) * TPB + wv / KSPLIT;      // row tile of this wave
+  const bool tile_ok = rt < a.n_rtiles;
   const int r = lane & 31, h = lane >> 5;
   int row0, row1;
   bool ok0, ok1;
@@ -77,98 +83,116 @@ mx_gemm_kernel(MxArgs a) {
   const uint8_t* s0 = a.S + (size_t)e * a.s_e + (size_t)row0 * a.s_ld;
   const uint8_t* s1 = a.S + (size_t)e * a.s_e + (size_t)row1 * a.s_ld;
   const int nc = a.K / 128;
-  const int c_begin = w * nc / 4, c_end = (w + 1) * nc / 4;
+  const int c_begin = w * nc / KSPLIT, c_end = tile_ok ? (w + 1) * nc / KSPLIT : c_begin;
 
   for (int mb = m_begin; mb < m_end; mb += 32) {
     const int m = mb + r;
     const bool tok = m < m_end;
-    const int xr = tok ? (a.x_gather ? a.x_gather[m] : m) : 0;
+    // Lanes past the group's last token read the first token's row: they only feed output
+    // columns that are never stored, and unconditional loads keep the pipeline's waits partial.
+    const int mm = tok ? m : m_begin;
+    const int xr = a.x_gather ? a.x_gather[mm] : mm;
     const bf16* xrow = a.X + (size_t)xr * a.x_ld;
     f32x16 acc0, acc1;
 #pragma unroll
     for (int v = 0; v < 16; ++v) { acc0[v] = 0.f; acc1[v] = 0.f; }
 
-    // Software pipeline: the weights of chunk c+1 are in flight while chunk c computes.
-    uint4 wa[4], wb[4], na[4], nb[4];
-    unsigned short sa = 0, sb = 0, nsa = 0, nsb = 0;
-    auto fetch = [&](int c, uint4 (&xa)[4], uint4 (&xb)[4], unsigned short& ta,
-                     unsigned short& tb) {
+    // Software pipeline over two register buffers (no copies): everything chunk c+1 needs (token
+    // fragments, weights, scales) is issued before chunk c computes. Vector loads retire in issue
+    // order, so chunk c waits only for loads issued an iteration earlier. The prefetch is
+    // unconditional (the last one re-reads a valid chunk) so every path has the same count of
+    // loads in flight and the compiler's waits stay partial.
+    struct Buf {
+      i32x4 x[8];
+      uint4 a[4], b[4];
+      unsigned short sa, sb;
+    };
+    Buf p0, p1;
+    auto fetch = [&](int c, Buf& f) {
       const int kb = c * 128 + h * 64;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f.x[j] = ldg16(xrow + kb + 8 * j);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        xa[i] = *(const uint4*)(w0 + kb + 16 * i);
-        xb[i] = *(const uint4*)(w1 + kb + 16 * i);
+        f.a[i] = *(const uint4*)(w0 + kb + 16 * i);
+        f.b[i] = *(const uint4*)(w1 + kb + 16 * i);
       }
-      ta = *(const unsigned short*)(s0 + kb / 32);
-      tb = *(const unsigned short*)(s1 + kb / 32);
+      f.sa = *(const unsigned short*)(s0 + kb / 32);
+      f.sb = *(const unsigned short*)(s1 + kb / 32);
+      __builtin_amdgcn_sched_barrier(0);  // issue the whole batch before the compute that follows
     };
-    if (c_begin < c_end) fetch(c_begin, wa, wb, sa, sb);
-    for (int c = c_begin; c < c_end; ++c) {
-      if (c + 1 < c_end) fetch(c + 1, na, nb, nsa, nsb);
-      const int kb = c * 128 + h * 64;
-      const float sa0 = e8m0_to_f32(sa & 0xff), sa1 = e8m0_to_f32(sa >> 8);
-      const float sb0 = e8m0_to_f32(sb & 0xff), sb1 = e8m0_to_f32(sb >> 8);
+    auto compute = [&](const Buf& f) {
+      const float sa0 = e8m0_to_f32(f.sa & 0xff), sa1 = e8m0_to_f32(f.sa >> 8);
+      const float sb0 = e8m0_to_f32(f.sb & 0xff), sb1 = e8m0_to_f32(f.sb >> 8);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const i32x4 xv = tok ? ldg16(xrow + kb + 8 * j) : zero4();
-        const uint4 ua = wa[j >> 1], ub = wb[j >> 1];
+        const uint4 ua = f.a[j >> 1], ub = f.b[j >> 1];
         const i32x4 av = (j & 1) ? dequant8(ua.z, ua.w, j < 4 ? sa0 : sa1)
                                  : dequant8(ua.x, ua.y, j < 4 ? sa0 : sa1);
         const i32x4 bv = (j & 1) ? dequant8(ub.z, ub.w, j < 4 ? sb0 : sb1)
                                  : dequant8(ub.x, ub.y, j < 4 ? sb0 : sb1);
-        Mfma<bf16>::step(acc0, av, xv);
-        Mfma<bf16>::step(acc1, bv, xv);
+        Mfma<bf16>::step(acc0, av, f.x[j]);
+        Mfma<bf16>::step(acc1, bv, f.x[j]);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { wa[i] = na[i]; wb[i] = nb[i]; }
-      sa = nsa;
-      sb = nsb;
+    };
+    const int c_last = c_end - 1;
+    if (c_begin <= c_last) {
+      fetch(c_begin, p0);
+      for (int c = c_begin; c <= c_last; c += 2) {
+        fetch(min(c + 1, c_last), p1);
+        compute(p0);
+        if (c + 1 > c_last) break;
+        fetch(min(c + 2, c_last), p0);
+        compute(p1);
+      }
     }
 
-    if (w > 0) {
-      red[w - 1][0][lane] = acc0;
-      red[w - 1][1][lane] = acc1;
-    }
-    __syncthreads();
-    if (w == 0) {
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        const f32x16 p0 = red[q][0][lane], p1 = red[q][1][lane];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) { acc0[v] += p0[v]; acc1[v] += p1[v]; }
+    if (KSPLIT > 1) {
+      if (w > 0) {
+        red[wv][0][lane] = acc0;
+        red[wv][1][lane] = acc1;
       }
-      if (tok) {
-        bf16* o = a.out + (size_t)m * a.out_ld;
+      __syncthreads();
+      if (w == 0) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int i0 = 8 * g + 4 * h;  // row within the 32-row tile
-          if (GLU) {
-            if (rt * 32 + i0 < a.I) {
-              float iv[4];
+        for (int q = 1; q < KSPLIT; ++q) {
+          const f32x16 p0 = red[wv + q][0][lane], p1 = red[wv + q][1][lane];
 #pragma unroll
-              for (int j = 0; j < 4; ++j) iv[j] = silu(acc0[4 * g + j]) * acc1[4 * g + j];
-              const bf16x2 p = {(bf16)iv[0], (bf16)iv[1]}, q = {(bf16)iv[2], (bf16)iv[3]};
-              *(uint2*)(o + rt * 32 + i0) =
-                  uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
-            }
-          } else {
-            if (rt * 64 + i0 < a.R) {
-              const bf16x2 p = {(bf16)acc0[4 * g], (bf16)acc0[4 * g + 1]};
-              const bf16x2 q = {(bf16)acc0[4 * g + 2], (bf16)acc0[4 * g + 3]};
-              *(uint2*)(o + rt * 64 + i0) =
-                  uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
-            }
-            if (rt * 64 + 32 + i0 < a.R) {
-              const bf16x2 p = {(bf16)acc1[4 * g], (bf16)acc1[4 * g + 1]};
-              const bf16x2 q = {(bf16)acc1[4 * g + 2], (bf16)acc1[4 * g + 3]};
-              *(uint2*)(o + rt * 64 + 32 + i0) =
-                  uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
-            }
+          for (int v = 0; v < 16; ++v) { acc0[v] += p0[v]; acc1[v] += p1[v]; }
+        }
+      }
+    }
+    if (w == 0 && tok && tile_ok) {
+      bf16* o = a.out + (size_t)m * a.out_ld;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i0 = 8 * g + 4 * h;  // row within the 32-row tile
+        if (GLU) {
+          if (rt * 32 + i0 < a.I) {
+            float iv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) iv[j] = silu(acc0[4 * g + j]) * acc1[4 * g + j];
+            const bf16x2 p = {(bf16)iv[0], (bf16)iv[1]}, q = {(bf16)iv[2], (bf16)iv[3]};
+            *(uint2*)(o + rt * 32 + i0) =
+                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
+          }
+        } else {
+          if (rt * 64 + i0 < a.R) {
+            const bf16x2 p = {(bf16)acc0[4 * g], (bf16)acc0[4 * g + 1]};
+            const bf16x2 q = {(bf16)acc0[4 * g + 2], (bf16)acc0[4 * g + 3]};
+            *(uint2*)(o + rt * 64 + i0) =
+                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
+          }
+          if (rt * 64 + 32 + i0 < a.R) {
+            const bf16x2 p = {(bf16)acc1[4 * g], (bf16)acc1[4 * g + 1]};
+            const bf16x2 q = {(bf16)acc1[4 * g + 2], (bf16)acc1[4 * g + 3]};
+            *(uint2*)(o + rt * 64 + 32 + i0) =
+                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
           }
         }
       }
     }
-    __syncthreads();
+    if (KSPLIT > 1) __syncthreads();
   }
 }
 
@@ -177,6 +201,18 @@ mx_gemm_kernel(MxArgs a) {
 using namespace moe;
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// ksplit = waves per row tile (4: each block is one row tile with K split four ways; measured
+// within a few percent of 2 and 1 for both kernels at the decode shape).
+template <bool GLU>
+static bool launch_mx(const MxArgs& a, int E, int ksplit, hipStream_t s) {
+  const int tpb = 4 / ksplit;
+  const unsigned grid = (unsigned)(E * ((a.n_rtiles + tpb - 1) / tpb));
+  if (ksplit == 1) hipLaunchKernelGGL((mx_gemm_kernel<GLU, 1>), dim3(grid), dim3(256), 0, s, a);
+  else if (ksplit == 2) hipLaunchKernelGGL((mx_gemm_kernel<GLU, 2>), dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((mx_gemm_kernel<GLU, 4>), dim3(grid), dim3(256), 0, s, a);
+  return hipGetLastError() == hipSuccess;
+}
 
 extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, const void* w13_q,
                              const void* w13_scale, const void* w2_q, const void* w2_scale, int E,
@@ -201,8 +237,7 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
   g.X = (const bf16*)hidden; g.x_ld = H; g.x_gather = sorted_token;
   g.offsets = offsets; g.n_rtiles = (int)((I + 31) / 32);
   g.out = (bf16*)inter; g.out_ld = I;
-  hipLaunchKernelGGL(mx_gemm_kernel<true>, dim3((unsigned)(E * g.n_rtiles)), dim3(256), 0, s, g);
-  if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
+  if (!launch_mx<true>(g, E, 4, s)) return MOE_ERR_LAUNCH;
   MxArgs d = {};
   d.W = (const uint8_t*)w2_q; d.w_e = H * I; d.w_ld = I;
   d.S = (const uint8_t*)w2_scale; d.s_e = H * (I / 32); d.s_ld = I / 32;
@@ -210,6 +245,5 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
   d.X = (const bf16*)inter; d.x_ld = I; d.x_gather = nullptr;
   d.offsets = offsets; d.n_rtiles = (int)((H + 63) / 64);
   d.out = (bf16*)eo; d.out_ld = H;
-  hipLaunchKernelGGL(mx_gemm_kernel<false>, dim3((unsigned)(E * d.n_rtiles)), dim3(256), 0, s, d);
-  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+  return launch_mx<false>(d, E, 4, s) ? MOE_OK : MOE_ERR_LAUNCH;
 }
