@@ -418,6 +418,107 @@ wgrad_kernel(WgradArgs a) {
 
 template <typename T> using V2Cfg = Cfg<T, v2::TILE, v2::TILE, 2, 2>;
 
+// Token-GEMM epilogue of the 256x256 kernels through LDS (v2::stage_acc): same values as
+// token_epilogue, written as whole 16-byte chunks. Wave (wr, wc) owns sorted rows
+// m0 + wc*128 + q and, per mode, these channels of its staged block:
+//   EPI_STORE   chunk c -> out channel rt*256 + wr*128 + 8c
+//   EPI_GLU_FWD chunk c < 8 -> gate channel rt*128 + wr*64 + 8c, chunk c + 8 -> the same up channel
+//   EPI_GLU_BWD chunk c -> grad_inter channel rt*256 + wr*128 + 8c
+template <typename T, int EPI>
+__device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][v2::TN], const TokenArgs& a,
+                                                  int e, int m0, int m_end, int rt, char* smem) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
+  char* wl = smem + w * (v2::WT * v2::EPI_ROWB);
+  const int row0 = m0 + wc * v2::WT;
+  v2::stage_acc<T>(acc, wl);
+  __syncthreads();
+  if constexpr (EPI == EPI_STORE) {
+    v2::store_staged<T>(wl, (T*)a.out, a.out_ld, row0, m_end, rt * v2::TILE + wr * v2::WT, a.R);
+  } else if constexpr (EPI == EPI_GLU_FWD) {
+    const int code = a.act_codes ? a.act_codes[e] : 0;
+    const int c = lane & 7;
+    const int ch = rt * (v2::TILE / 2) + wr * (v2::WT / 2) + 8 * c;
+    T* gu = (T*)a.out;
+    T* it = (T*)a.out2;
+#pragma unroll 4
+    for (int i = 0; i < v2::WT / 8; ++i) {
+      const int q = i * 8 + (lane >> 3);
+      const int m = row0 + q;
+      const i32x4 gq = v2::staged(wl, q, c), uq = v2::staged(wl, q, c + 8);
+      if (m < m_end && ch < a.I) {
+        T* r = gu + (size_t)m * 2 * a.I + ch;
+        *(i32x4*)r = gq;
+        *(i32x4*)(r + a.I) = uq;
+        if (it) {
+          float gv[8], uv[8], iv[8];
+          v2::unpack8<T>(gq, gv);
+          v2::unpack8<T>(uq, uv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) iv[j] = glu_act(code, gv[j]) * uv[j];
+          *(i32x4*)(it + (size_t)m * a.I + ch) = v2::pack8<T>(iv);
+        }
+      }
+    }
+  } else {  // EPI_GLU_BWD
+    const int code = a.act_codes ? a.act_codes[e] : 0;
+    const int c = lane & 15;
+    const int ch = rt * v2::TILE + wr * v2::WT + 8 * c;
+    const int chc = min(ch, a.I - 8);
+    const T* gu = (const T*)a.aux;
+    T* ggu = (T*)a.out;
+    T* gi = (T*)a.out2;
+    constexpr int NB = 8;  // rows per batch of loads
+#pragma unroll 1
+    for (int i0 = 0; i0 < v2::WT / 4; i0 += NB) {
+      i32x4 gq[NB], uq[NB];
+      if (ggu) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int m = min(row0 + (i0 + b) * 4 + (lane >> 4), m_end - 1);
+          const T* r = gu + (size_t)m * 2 * a.I + chc;
+          gq[b] = *(const i32x4*)r;
+          uq[b] = *(const i32x4*)(r + a.I);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int q = (i0 + b) * 4 + (lane >> 4);
+        const int m = row0 + q;
+        const i32x4 oq = v2::staged(wl, q, c);
+        if (m < m_end && ch < a.I) {
+          if (gi) *(i32x4*)(gi + (size_t)m * a.I + ch) = oq;
+          if (ggu) {
+            float go[8], gv[8], uv[8], dg[8], du[8];
+            v2::unpack8<T>(oq, go);
+            v2::unpack8<T>(gq[b], gv);
+            v2::unpack8<T>(uq[b], uv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              dg[j] = go[j] * uv[j] * glu_dact(code, gv[j]);
+              du[j] = go[j] * glu_act(code, gv[j]);
+            }
+            T* r = ggu + (size_t)m * 2 * a.I + ch;
+            *(i32x4*)r = v2::pack8<T>(dg);
+            *(i32x4*)(r + a.I) = v2::pack8<T>(du);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Weight-gradient epilogue of the 256x256 kernel: out[e, c, r], c = MFMA column, r contiguous.
+template <typename T>
+__device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][v2::TN], const WgradArgs& a,
+                                                  int e, int r0, int c0, char* smem) {
+  const int w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
+  char* wl = smem + w * (v2::WT * v2::EPI_ROWB);
+  v2::stage_acc<T>(acc, wl);
+  __syncthreads();
+  v2::store_staged<T>(wl, (T*)a.out + (size_t)e * a.C * a.R, a.R, c0 + wc * v2::WT, a.C,
+                      r0 + wr * v2::WT, a.R);
+}
+
 template <typename T, int EPI, bool P_RC>
 __global__ void __launch_bounds__(v2::NT, 1)
 token_gemm_v2_kernel(TokenArgs a, int n_logical) {
@@ -488,13 +589,12 @@ token_gemm_v2_kernel(TokenArgs a, int n_logical) {
     }
     v2::mainloop<T>(acc, lp, lq, 0, a.K, smem);
   }
-  token_epilogue<C, EPI>(acc, a, e, m0, m_end, rt);
+  token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem);
 }
 
 template <typename T, bool RG, bool CG>
 __global__ void __launch_bounds__(v2::NT, 1)
 wgrad_v2_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
-  using C = V2Cfg<T>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
   // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
@@ -529,7 +629,7 @@ wgrad_v2_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
   v2::mainloop<T>(acc, lp, lq, k0, k1, smem);
-  wgrad_epilogue<C>(acc, a, e, r0, c0);
+  wgrad_epilogue_v2<T>(acc, a, e, r0, c0, smem);
 }
 
 // ---------------------------------------------------------------------------------------------

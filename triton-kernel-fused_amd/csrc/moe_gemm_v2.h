@@ -196,6 +196,89 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[TN][TN], LP& lp, LQ& lq, 
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Epilogue staging. The MFMA accumulator gives a lane four consecutive output channels of one
+// output row, so storing it directly writes 8 bytes into each of 32 rows per instruction. Instead
+// each wave writes its 128x128 block, rounded to T, into its own 32 KB of LDS transposed to
+// [q][p] (q = MFMA column = output row, p = MFMA row = output channel; 256 bytes per q row, the
+// 16-byte chunk index XOR-ed by (q & 15), so the 8-byte writes of 32 lanes cover all 64 banks
+// once), and reads it back as 16-byte chunks with 16 lanes per row: every store instruction then
+// writes whole 256-byte row segments.
+constexpr int EPI_ROWB = WT * 2;  // bytes per staged row
+
+template <typename T> __device__ __forceinline__ unsigned pack2(float a, float b);
+template <> __device__ __forceinline__ unsigned pack2<bf16>(float a, float b) {
+  return __builtin_bit_cast(unsigned, bf16x2{(bf16)a, (bf16)b});
+}
+template <> __device__ __forceinline__ unsigned pack2<f16>(float a, float b) {
+  typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
+  return __builtin_bit_cast(unsigned, h2{(f16)a, (f16)b});
+}
+
+// Eight 16-bit values of a 16-byte chunk as floats (whole-word conversions only).
+template <typename T> __device__ __forceinline__ void unpack8(i32x4 v, float (&f)[8]);
+template <> __device__ __forceinline__ void unpack8<bf16>(i32x4 v, float (&f)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const unsigned u = (unsigned)v[w];
+    f[2 * w] = __builtin_bit_cast(float, u << 16);
+    f[2 * w + 1] = __builtin_bit_cast(float, u & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack8<f16>(i32x4 v, float (&f)[8]) {
+  typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const h2 h = __builtin_bit_cast(h2, (unsigned)v[w]);
+    f[2 * w] = (float)h[0];
+    f[2 * w + 1] = (float)h[1];
+  }
+}
+template <typename T> __device__ __forceinline__ i32x4 pack8(const float (&f)[8]) {
+  return i32x4{(int)pack2<T>(f[0], f[1]), (int)pack2<T>(f[2], f[3]), (int)pack2<T>(f[4], f[5]),
+               (int)pack2<T>(f[6], f[7])};
+}
+
+__device__ __forceinline__ int staged_off(int q, int c) { return q * EPI_ROWB + ((c ^ (q & 15)) << 4); }
+
+// Write this wave's accumulators to its LDS block wl (the mainloop's last barrier has released
+// the LDS). Channel p = ti*32 + 8g + 4h + j sits in chunk p/8 = 4ti + g, half h.
+template <typename T>
+__device__ __forceinline__ void stage_acc(const f32x16 (&acc)[TN][TN], char* wl) {
+  const int lane = threadIdx.x & 63, h = lane >> 5;
+#pragma unroll
+  for (int tj = 0; tj < TN; ++tj) {
+    const int q = tj * 32 + (lane & 31);
+#pragma unroll
+    for (int ti = 0; ti < TN; ++ti)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 v = {pack2<T>(acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1]),
+                   pack2<T>(acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3])};
+        *(uint2*)(wl + staged_off(q, 4 * ti + g) + 8 * h) = v;
+      }
+  }
+}
+
+__device__ __forceinline__ i32x4 staged(const char* wl, int q, int c) {
+  return *(const i32x4*)(wl + staged_off(q, c));
+}
+
+// Plain store of a staged block: out row (row0 + q) gets channels ch0 + 8c .. +7 for the rows
+// below row_end and channels below n_ch (a multiple of 8).
+template <typename T>
+__device__ __forceinline__ void store_staged(const char* wl, T* out, long long ld, int row0,
+                                             int row_end, int ch0, int n_ch) {
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  const int ch = ch0 + 8 * c;
+#pragma unroll 8
+  for (int it = 0; it < WT / 4; ++it) {
+    const int q = it * 4 + (lane >> 4);
+    const i32x4 v = staged(wl, q, c);
+    if (row0 + q < row_end && ch < n_ch) *(i32x4*)(out + (size_t)(row0 + q) * ld + ch) = v;
+  }
+}
+
 // Block -> logical tile with XCD grouping: workgroups are dealt to the 8 XCDs round-robin, so
 // logical = (b % 8) * (G8 / 8) + b / 8 gives every XCD a contiguous run of logical tiles (shared
 // operands stay in that XCD's L2). G8 = gridDim.x, a multiple of 8.
