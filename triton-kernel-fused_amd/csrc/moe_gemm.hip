@@ -15,7 +15,7 @@
 // exits if its tile is past the end, so the grid is a host-side upper bound and nothing syncs.
 #include "moe_common.h"
 #include "moe_gemm_common.h"
-#include "moe_gemm_v2.h"
+#include "moe_gemm_v3.h"
 
 namespace moe {
 
@@ -519,9 +519,12 @@ __device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][v2
                       r0 + wr * v2::WT, a.R);
 }
 
+// Forward GEMMs (both operands K-contiguous): 64-element K steps double-buffered, so every DMA
+// request is a whole 128-byte line.
 template <typename T, int EPI, bool P_RC>
 __global__ void __launch_bounds__(v2::NT, 1)
 token_gemm_v2_kernel(TokenArgs a, int n_logical) {
+  static_assert(!P_RC, "the 256x256 / BK=64 kernel serves the forward (both operands K-contiguous)");
   using C = V2Cfg<T>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
@@ -562,16 +565,7 @@ token_gemm_v2_kernel(TokenArgs a, int n_logical) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
 
-  if constexpr (P_RC) {
-    v2::RcReg<false> lp;
-    const int r0 = rt * v2::TILE;
-    lp.src = (const char*)(Pe + r0);
-    lp.ld = (size_t)a.p_ld * sizeof(T);
-    lp.gather = nullptr;
-    lp.kend = a.K;
-    lp.init(a.R - r0);
-    v2::mainloop<T>(acc, lp, lq, 0, a.K, smem);
-  } else {
+  {
     v2::DmaKc lp;
     lp.init();
 #pragma unroll
@@ -592,10 +586,85 @@ token_gemm_v2_kernel(TokenArgs a, int n_logical) {
   token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem);
 }
 
+// dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.
+template <typename T, int EPI, bool P_RC>
+__global__ void __launch_bounds__(v3::NT, 1)
+token_gemm_v3_kernel(TokenArgs a, int n_logical) {
+  using C = V2Cfg<T>;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int lid = v3::xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  if (lid >= n_logical) return;
+  // The expert tile scan borrows the last LDS stage (free until the K loop's prologue).
+  int* s_pref = (int*)(smem + (v3::NSTAGE - 1) * v3::STAGEB);
+  tile_prefix<v3::NT>(a.offsets, a.E_glu, v3::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
+  const int mt = lid / a.n_rtiles;
+  const int rt = lid % a.n_rtiles;
+  if (mt >= s_pref[a.E_glu]) return;
+  int lo = 0, hi = a.E_glu - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
+  }
+  const int e = lo;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v3::TILE;
+  const int m_end = a.offsets[e + 1];
+  const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
+  const int w = (int)threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
+
+  // Token rows past the group end read row m0 (their results are never stored).
+  v3::KcDma lq;
+  lq.init(wc * v3::WT);
+#pragma unroll
+  for (int i = 0; i < v3::LOADS; ++i) {
+    int m = m0 + v3::KcDma::row_of(i);
+    if (m >= m_end) m = m0;
+    const int qr = a.q_gather ? a.q_gather[m] : m;
+    lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
+  }
+
+  f32x16 acc[v3::TN][v3::TN];
+#pragma unroll
+  for (int ti = 0; ti < v3::TN; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < v3::TN; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+
+  if constexpr (P_RC) {
+    v3::RcDma<false> lp;
+    const int r0 = rt * v3::TILE;
+    lp.src = (const char*)(Pe + r0);
+    lp.ld = (size_t)a.p_ld * sizeof(T);
+    lp.gather = nullptr;
+    lp.kend = a.K;
+    lp.init(wr * v3::WT, a.R - r0);
+    v3::mainloop<T>(acc, lp, lq, 0, a.K, smem);
+  } else {
+    v3::KcDma lp;
+    lp.init(wr * v3::WT);
+#pragma unroll
+    for (int i = 0; i < v3::LOADS; ++i) {
+      const int rr = v3::KcDma::row_of(i);
+      bool ok;
+      int prow;
+      if (EPI == EPI_GLU_FWD) {
+        prow = glu_prow<C>(rr, rt, a.I, ok);
+      } else {
+        prow = rt * v3::TILE + rr;
+        ok = prow < a.R;
+      }
+      lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+    }
+    v3::mainloop<T>(acc, lp, lq, 0, a.K, smem);
+  }
+  token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem);
+}
+
 template <typename T, bool RG, bool CG>
-__global__ void __launch_bounds__(v2::NT, 1)
-wgrad_v2_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+__global__ void __launch_bounds__(v3::NT, 1)
+wgrad_v3_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
   // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
   // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
   const int lid = (int)blockIdx.x;
@@ -606,29 +675,30 @@ wgrad_v2_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
   if (e < 0 || e >= E_glu) return;  // weightless special expert
   const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
   const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
-  const int r0 = rt * v2::TILE, c0 = ct * v2::TILE;
+  const int r0 = rt * v3::TILE, c0 = ct * v3::TILE;
+  const int w = (int)threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
 
-  v2::RcReg<RG> lp;
+  v3::RcDma<RG> lp;
   lp.src = (const char*)((const T*)a.rsrc + r0);
   lp.ld = (size_t)a.r_ld * sizeof(T);
   lp.gather = a.r_gather;
   lp.kend = k1;
-  lp.init(a.R - r0);
-  v2::RcReg<CG> lq;
+  lp.init(wr * v3::WT, a.R - r0);
+  v3::RcDma<CG> lq;
   lq.src = (const char*)((const T*)a.csrc + c0);
   lq.ld = (size_t)a.c_ld * sizeof(T);
   lq.gather = a.c_gather;
   lq.kend = k1;
-  lq.init(a.C - c0);
+  lq.init(wc * v3::WT, a.C - c0);
 
-  f32x16 acc[v2::TN][v2::TN];
+  f32x16 acc[v3::TN][v3::TN];
 #pragma unroll
-  for (int ti = 0; ti < v2::TN; ++ti)
+  for (int ti = 0; ti < v3::TN; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < v2::TN; ++tj)
+    for (int tj = 0; tj < v3::TN; ++tj)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-  v2::mainloop<T>(acc, lp, lq, k0, k1, smem);
+  v3::mainloop<T>(acc, lp, lq, k0, k1, smem);
   wgrad_epilogue_v2<T>(acc, a, e, r0, c0, smem);
 }
 
@@ -671,9 +741,15 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   if (logical <= 0 || n_rows == 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  auto kern = token_gemm_v2_kernel<T, EPI, P_RC>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+  if constexpr (P_RC) {
+    auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, (int)logical);
+  } else {
+    auto kern = token_gemm_v2_kernel<T, EPI, P_RC>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+  }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -686,10 +762,10 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
   if (logical <= 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  auto kern = a.r_gather ? (a.c_gather ? wgrad_v2_kernel<T, true, true> : wgrad_v2_kernel<T, true, false>)
-                         : (a.c_gather ? wgrad_v2_kernel<T, false, true> : wgrad_v2_kernel<T, false, false>);
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, order, E_glu,
+  auto kern = a.r_gather ? (a.c_gather ? wgrad_v3_kernel<T, true, true> : wgrad_v3_kernel<T, true, false>)
+                         : (a.c_gather ? wgrad_v3_kernel<T, false, true> : wgrad_v3_kernel<T, false, false>);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, order, E_glu,
                      (int)logical);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
@@ -808,7 +884,7 @@ extern "C" int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo,
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {
-      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_GLU_BWD, true>(a, n_rows, s);
+      if (a.K % v3::KS == 0) return launch_token_v2<T, EPI_GLU_BWD, true>(a, n_rows, s);
     }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((I + C::BR - 1) / C::BR);
@@ -840,7 +916,7 @@ extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gat
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {
-      if (a.K % v2::BK == 0) return launch_token_v2<T, EPI_STORE, true>(a, n_rows, s);
+      if (a.K % v3::KS == 0) return launch_token_v2<T, EPI_STORE, true>(a, n_rows, s);
     }
     using C = TokCfg<T>;
     a.n_rtiles = (int)((H + C::BR - 1) / C::BR);
