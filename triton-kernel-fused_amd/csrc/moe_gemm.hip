@@ -16,6 +16,9 @@
 #include "moe_common.h"
 #include "moe_gemm_common.h"
 #include "moe_gemm_v3.h"
+#include "moe_gemm_v4.h"
+
+
 
 namespace moe {
 
@@ -424,16 +427,20 @@ template <typename T> using V2Cfg = Cfg<T, v2::TILE, v2::TILE, 2, 2>;
 //   EPI_STORE   chunk c -> out channel rt*256 + wr*128 + 8c
 //   EPI_GLU_FWD chunk c < 8 -> gate channel rt*128 + wr*64 + 8c, chunk c + 8 -> the same up channel
 //   EPI_GLU_BWD chunk c -> grad_inter channel rt*256 + wr*128 + 8c
-template <typename T, int EPI>
-__device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][v2::TN], const TokenArgs& a,
-                                                  int e, int m0, int m_end, int rt, char* smem) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
-  char* wl = smem + w * (v2::WT * v2::EPI_ROWB);
-  const int row0 = m0 + wc * v2::WT;
-  v2::stage_acc<T>(acc, wl);
+// TJ = 32-row token tiles per wave (WQ = 32 TJ token rows); the wave holds channels wr*128..+127
+// of the 256-channel tile and token rows wc*WQ..+WQ-1.
+template <typename T, int EPI, int TJ = v2::TN>
+__device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ], const TokenArgs& a,
+                                                  int e, int m0, int m_end, int rt, char* smem,
+                                                  int wr, int wc) {
+  constexpr int WQ = 32 * TJ;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  char* wl = smem + w * (WQ * v2::EPI_ROWB);
+  const int row0 = m0 + wc * WQ;
+  v2::stage_acc<T, TJ>(acc, wl);
   __syncthreads();
   if constexpr (EPI == EPI_STORE) {
-    v2::store_staged<T>(wl, (T*)a.out, a.out_ld, row0, m_end, rt * v2::TILE + wr * v2::WT, a.R);
+    v2::store_staged<T, WQ>(wl, (T*)a.out, a.out_ld, row0, m_end, rt * v2::TILE + wr * v2::WT, a.R);
   } else if constexpr (EPI == EPI_GLU_FWD) {
     const int code = a.act_codes ? a.act_codes[e] : 0;
     const int c = lane & 7;
@@ -441,7 +448,7 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][v2
     T* gu = (T*)a.out;
     T* it = (T*)a.out2;
 #pragma unroll 4
-    for (int i = 0; i < v2::WT / 8; ++i) {
+    for (int i = 0; i < WQ / 8; ++i) {
       const int q = i * 8 + (lane >> 3);
       const int m = row0 + q;
       const i32x4 gq = v2::staged(wl, q, c), uq = v2::staged(wl, q, c + 8);
@@ -469,7 +476,7 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][v2
     T* gi = (T*)a.out2;
     constexpr int NB = 8;  // rows per batch of loads
 #pragma unroll 1
-    for (int i0 = 0; i0 < v2::WT / 4; i0 += NB) {
+    for (int i0 = 0; i0 < WQ / 4; i0 += NB) {
       i32x4 gq[NB], uq[NB];
       if (ggu) {
 #pragma unroll
@@ -519,20 +526,17 @@ __device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][v2
                       r0 + wr * v2::WT, a.R);
 }
 
-// Forward GEMMs (both operands K-contiguous): 64-element K steps double-buffered, so every DMA
-// request is a whole 128-byte line.
-template <typename T, int EPI, bool P_RC>
-__global__ void __launch_bounds__(v2::NT, 1)
-token_gemm_v2_kernel(TokenArgs a, int n_logical) {
-  static_assert(!P_RC, "the 256x256 / BK=64 kernel serves the forward (both operands K-contiguous)");
+// Forward GEMMs on the eight-wave kernel of moe_gemm_v4.h (both operands K-contiguous).
+template <typename T, int EPI>
+__global__ void __launch_bounds__(v4::NT, 1)
+token_gemm_v4_kernel(TokenArgs a, int n_logical) {
   using C = V2Cfg<T>;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
-  __shared__ int s_wsum[v2::NT / 64];
-
-  tile_prefix<v2::NT>(a.offsets, a.E_glu, v2::TILE, s_pref, s_wsum);
-  const int lid = v2::xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int lid = v4::xcd_logical((int)blockIdx.x, (int)gridDim.x);
   if (lid >= n_logical) return;
+  // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
+  int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
+  tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
   const int mt = lid / a.n_rtiles;
   const int rt = lid % a.n_rtiles;
   if (mt >= s_pref[a.E_glu]) return;
@@ -542,48 +546,46 @@ token_gemm_v2_kernel(TokenArgs a, int n_logical) {
     if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
   }
   const int e = lo;
-  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v2::TILE;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v4::TILE;
   const int m_end = a.offsets[e + 1];
   const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
 
   // Token rows past the group end read row m0 (their results are never stored).
-  v2::DmaKc lq;
+  v4::DmaKc lq;
   lq.init();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int m = m0 + v2::DmaKc::row_of(i);
+  for (int i = 0; i < v4::LOADS; ++i) {
+    int m = m0 + v4::DmaKc::row_of(i);
     if (m >= m_end) m = m0;
     const int qr = a.q_gather ? a.q_gather[m] : m;
     lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
   }
+  v4::DmaKc lp;
+  lp.init();
+#pragma unroll
+  for (int i = 0; i < v4::LOADS; ++i) {
+    const int rr = v4::DmaKc::row_of(i);
+    bool ok;
+    int prow;
+    if (EPI == EPI_GLU_FWD) {
+      prow = glu_prow<C>(rr, rt, a.I, ok);
+    } else {
+      prow = rt * v4::TILE + rr;
+      ok = prow < a.R;
+    }
+    lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+  }
 
-  f32x16 acc[v2::TN][v2::TN];
+  f32x16 acc[v4::TI][v4::TJ];
 #pragma unroll
-  for (int ti = 0; ti < v2::TN; ++ti)
+  for (int ti = 0; ti < v4::TI; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < v2::TN; ++tj)
+    for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-
-  {
-    v2::DmaKc lp;
-    lp.init();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = v2::DmaKc::row_of(i);
-      bool ok;
-      int prow;
-      if (EPI == EPI_GLU_FWD) {
-        prow = glu_prow<C>(rr, rt, a.I, ok);
-      } else {
-        prow = rt * v2::TILE + rr;
-        ok = prow < a.R;
-      }
-      lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
-    }
-    v2::mainloop<T>(acc, lp, lq, 0, a.K, smem);
-  }
-  token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem);
+  __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+  v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
+  token_epilogue_v2<T, EPI, v4::TJ>(acc, a, e, m0, m_end, rt, smem, v4::wave_r(), v4::wave_c());
 }
 
 // dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.
@@ -658,7 +660,7 @@ token_gemm_v3_kernel(TokenArgs a, int n_logical) {
     }
     v3::mainloop<T>(acc, lp, lq, 0, a.K, smem);
   }
-  token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem);
+  token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem, (int)(threadIdx.x >> 7), (int)(threadIdx.x >> 6) & 1);
 }
 
 template <typename T, bool RG, bool CG>
@@ -746,9 +748,9 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, (int)logical);
   } else {
-    auto kern = token_gemm_v2_kernel<T, EPI, P_RC>;
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+    auto kern = token_gemm_v4_kernel<T, EPI>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, (int)logical);
   }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }

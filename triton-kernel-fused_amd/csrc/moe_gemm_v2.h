@@ -41,6 +41,19 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// One direct-to-LDS load: lane l copies 16 bytes from g to LDS byte (l_base + 16 l); l_base is
+// wave-uniform. Written as inline asm so that the compiler does not track it: its own tracking
+// treats every later LDS read as dependent on every DMA in flight and waits for all of them,
+// which would drain the pipeline each step. The K loops order these loads themselves with
+// explicit vmcnt waits.
+__device__ __forceinline__ void dma16(const void* g, char* l_base) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)l_base;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(m0)
+               : "memory", "m0");
+}
+
 // K-contiguous operand loaded by DMA. Lane l of wave w fills tile row R = w*64 + i*8 + l/8 (i < 8),
 // physical chunk l%8, i.e. logical chunk (l%8) ^ ((R >> 1) & 7) = (l%8) ^ ((4*(i&1) + l/16) & 7).
 struct DmaKc {
@@ -243,11 +256,11 @@ __device__ __forceinline__ int staged_off(int q, int c) { return q * EPI_ROWB + 
 
 // Write this wave's accumulators to its LDS block wl (the mainloop's last barrier has released
 // the LDS). Channel p = ti*32 + 8g + 4h + j sits in chunk p/8 = 4ti + g, half h.
-template <typename T>
-__device__ __forceinline__ void stage_acc(const f32x16 (&acc)[TN][TN], char* wl) {
+template <typename T, int TJ = TN>
+__device__ __forceinline__ void stage_acc(const f32x16 (&acc)[TN][TJ], char* wl) {
   const int lane = threadIdx.x & 63, h = lane >> 5;
 #pragma unroll
-  for (int tj = 0; tj < TN; ++tj) {
+  for (int tj = 0; tj < TJ; ++tj) {
     const int q = tj * 32 + (lane & 31);
 #pragma unroll
     for (int ti = 0; ti < TN; ++ti)
@@ -264,15 +277,15 @@ __device__ __forceinline__ i32x4 staged(const char* wl, int q, int c) {
   return *(const i32x4*)(wl + staged_off(q, c));
 }
 
-// Plain store of a staged block: out row (row0 + q) gets channels ch0 + 8c .. +7 for the rows
-// below row_end and channels below n_ch (a multiple of 8).
-template <typename T>
+// Plain store of a staged block of WQ rows: out row (row0 + q) gets channels ch0 + 8c .. +7 for
+// the rows below row_end and channels below n_ch (a multiple of 8).
+template <typename T, int WQ = WT>
 __device__ __forceinline__ void store_staged(const char* wl, T* out, long long ld, int row0,
                                              int row_end, int ch0, int n_ch) {
   const int lane = threadIdx.x & 63, c = lane & 15;
   const int ch = ch0 + 8 * c;
 #pragma unroll 8
-  for (int it = 0; it < WT / 4; ++it) {
+  for (int it = 0; it < WQ / 4; ++it) {
     const int q = it * 4 + (lane >> 4);
     const i32x4 v = staged(wl, q, c);
     if (row0 + q < row_end && ch < n_ch) *(i32x4*)(out + (size_t)(row0 + q) * ld + ch) = v;

@@ -54,19 +54,7 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 typedef const __attribute__((address_space(4))) int32_t cint32;
 __device__ __forceinline__ int sload(const int32_t* p) { return *(cint32*)p; }
 
-// One direct-to-LDS load: lane l copies 16 bytes from g to LDS byte (l_base + 16 l). Written as
-// inline asm so that the compiler does not track it: its own tracking treats every later LDS
-// transpose read as dependent on every DMA in flight and waits for all of them, which would
-// drain the pipeline each step. The K loop orders these loads itself with explicit vmcnt waits
-// (the counter retires in issue order, so a compiler-generated wait for its own loads can only
-// over-wait, never under-wait).
-__device__ __forceinline__ void dma16(const void* g, char* l_base) {
-  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)l_base;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(m0)
-               : "memory", "m0");
-}
+using v2::dma16;
 
 // ---------------------------------------------------------------------------------------------
 // K-contiguous operand. Lane l of wave w fills row w*64 + 16i + l/4 (i < 4), physical chunk l%4,
