@@ -515,19 +515,23 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
 }
 
 // Weight-gradient epilogue of the 256x256 kernel: out[e, c, r], c = MFMA column, r contiguous.
-template <typename T>
-__device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][v2::TN], const WgradArgs& a,
-                                                  int e, int r0, int c0, char* smem) {
-  const int w = threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
-  char* wl = smem + w * (v2::WT * v2::EPI_ROWB);
-  v2::stage_acc<T>(acc, wl);
+// TJ = 32-column tiles per wave (WQ = 32 TJ output rows c); the wave holds r = wr*128..+127.
+template <typename T, int TJ = v2::TN>
+__device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ], const WgradArgs& a,
+                                                  int e, int r0, int c0, char* smem, int wr, int wc) {
+  constexpr int WQ = 32 * TJ;
+  const int w = threadIdx.x >> 6;
+  char* wl = smem + w * (WQ * v2::EPI_ROWB);
+  v2::stage_acc<T, TJ>(acc, wl);
   __syncthreads();
-  v2::store_staged<T>(wl, (T*)a.out + (size_t)e * a.C * a.R, a.R, c0 + wc * v2::WT, a.C,
-                      r0 + wr * v2::WT, a.R);
+  v2::store_staged<T, WQ>(wl, (T*)a.out + (size_t)e * a.C * a.R, a.R, c0 + wc * WQ, a.C,
+                          r0 + wr * v2::WT, a.R);
 }
 
-// Forward GEMMs on the eight-wave kernel of moe_gemm_v4.h (both operands K-contiguous).
-template <typename T, int EPI>
+// Token GEMMs on the eight-wave ring kernel of moe_gemm_v4.h. The token side Q is K-contiguous
+// (gathered or sorted rows); the weights P are K-contiguous in the forward and row-contiguous
+// (P_RC) in the dX GEMMs.
+template <typename T, int EPI, bool P_RC>
 __global__ void __launch_bounds__(v4::NT, 1)
 token_gemm_v4_kernel(TokenArgs a, int n_logical) {
   using C = V2Cfg<T>;
@@ -549,31 +553,17 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
   const int m0 = a.offsets[e] + (mt - s_pref[e]) * v4::TILE;
   const int m_end = a.offsets[e + 1];
   const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
+  const int wr = v4::wave_r(), wc = v4::wave_c();
 
   // Token rows past the group end read row m0 (their results are never stored).
-  v4::DmaKc lq;
-  lq.init();
+  v4::KcLoad lq;
+  lq.init(wc * v4::WQ);
 #pragma unroll
   for (int i = 0; i < v4::LOADS; ++i) {
-    int m = m0 + v4::DmaKc::row_of(i);
+    int m = m0 + v4::KcLoad::row_of(i);
     if (m >= m_end) m = m0;
     const int qr = a.q_gather ? a.q_gather[m] : m;
     lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
-  }
-  v4::DmaKc lp;
-  lp.init();
-#pragma unroll
-  for (int i = 0; i < v4::LOADS; ++i) {
-    const int rr = v4::DmaKc::row_of(i);
-    bool ok;
-    int prow;
-    if (EPI == EPI_GLU_FWD) {
-      prow = glu_prow<C>(rr, rt, a.I, ok);
-    } else {
-      prow = rt * v4::TILE + rr;
-      ok = prow < a.R;
-    }
-    lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
   }
 
   f32x16 acc[v4::TI][v4::TJ];
@@ -583,9 +573,80 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
     for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-  __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
-  v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
-  token_epilogue_v2<T, EPI, v4::TJ>(acc, a, e, m0, m_end, rt, smem, v4::wave_r(), v4::wave_c());
+
+  if constexpr (P_RC) {
+    v4::RcLoad<false, v4::TI> lp;
+    const int r0 = rt * v4::TILE;
+    lp.src = (const char*)(Pe + r0);
+    lp.ld = (size_t)a.p_ld * sizeof(T);
+    lp.gather = nullptr;
+    lp.kend = a.K;
+    lp.init(wr * v4::WP, a.R - r0);
+    __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+    v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
+  } else {
+    v4::KcLoad lp;
+    lp.init(wr * v4::WP);
+#pragma unroll
+    for (int i = 0; i < v4::LOADS; ++i) {
+      const int rr = v4::KcLoad::row_of(i);
+      bool ok;
+      int prow;
+      if (EPI == EPI_GLU_FWD) {
+        prow = glu_prow<C>(rr, rt, a.I, ok);
+      } else {
+        prow = rt * v4::TILE + rr;
+        ok = prow < a.R;
+      }
+      lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+    }
+    __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+    v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
+  }
+  token_epilogue_v2<T, EPI, v4::TJ>(acc, a, e, m0, m_end, rt, smem, wr, wc);
+}
+
+// Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
+// of rsrc[rrow(m), r] * csrc[crow(m), c]; both operands row-contiguous (optionally gathered rows).
+template <typename T, bool RG, bool CG>
+__global__ void __launch_bounds__(v4::NT, 1)
+wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
+  // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
+  const int lid = (int)blockIdx.x;
+  if (lid >= n_logical) return;
+  const int per_e = a.n_rtiles * a.n_ctiles;
+  const int ei = lid / per_e, rem = lid % per_e;
+  const int e = order ? order[ei] : ei;
+  if (e < 0 || e >= E_glu) return;  // weightless special expert
+  const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
+  const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
+  const int r0 = rt * v4::TILE, c0 = ct * v4::TILE;
+  const int wr = v4::wave_r(), wc = v4::wave_c();
+
+  v4::RcLoad<RG, v4::TI> lp;
+  lp.src = (const char*)((const T*)a.rsrc + r0);
+  lp.ld = (size_t)a.r_ld * sizeof(T);
+  lp.gather = a.r_gather;
+  lp.kend = k1;
+  lp.init(wr * v4::WP, a.R - r0);
+  v4::RcLoad<CG, v4::TJ> lq;
+  lq.src = (const char*)((const T*)a.csrc + c0);
+  lq.ld = (size_t)a.c_ld * sizeof(T);
+  lq.gather = a.c_gather;
+  lq.kend = k1;
+  lq.init(wc * v4::WQ, a.C - c0);
+
+  f32x16 acc[v4::TI][v4::TJ];
+#pragma unroll
+  for (int ti = 0; ti < v4::TI; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < v4::TJ; ++tj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  v4::mainloop_ring<T>(acc, lp, lq, k0, k1, smem);
+  wgrad_epilogue_v2<T, v4::TJ>(acc, a, e, r0, c0, smem, wr, wc);
 }
 
 // dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.
@@ -663,47 +724,6 @@ token_gemm_v3_kernel(TokenArgs a, int n_logical) {
   token_epilogue_v2<T, EPI>(acc, a, e, m0, m_end, rt, smem, (int)(threadIdx.x >> 7), (int)(threadIdx.x >> 6) & 1);
 }
 
-template <typename T, bool RG, bool CG>
-__global__ void __launch_bounds__(v3::NT, 1)
-wgrad_v3_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
-  // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
-  // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
-  const int lid = (int)blockIdx.x;
-  if (lid >= n_logical) return;
-  const int per_e = a.n_rtiles * a.n_ctiles;
-  const int ei = lid / per_e, rem = lid % per_e;
-  const int e = order ? order[ei] : ei;
-  if (e < 0 || e >= E_glu) return;  // weightless special expert
-  const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
-  const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
-  const int r0 = rt * v3::TILE, c0 = ct * v3::TILE;
-  const int w = (int)threadIdx.x >> 6, wr = w >> 1, wc = w & 1;
-
-  v3::RcDma<RG> lp;
-  lp.src = (const char*)((const T*)a.rsrc + r0);
-  lp.ld = (size_t)a.r_ld * sizeof(T);
-  lp.gather = a.r_gather;
-  lp.kend = k1;
-  lp.init(wr * v3::WT, a.R - r0);
-  v3::RcDma<CG> lq;
-  lq.src = (const char*)((const T*)a.csrc + c0);
-  lq.ld = (size_t)a.c_ld * sizeof(T);
-  lq.gather = a.c_gather;
-  lq.kend = k1;
-  lq.init(wc * v3::WT, a.C - c0);
-
-  f32x16 acc[v3::TN][v3::TN];
-#pragma unroll
-  for (int ti = 0; ti < v3::TN; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < v3::TN; ++tj)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-  v3::mainloop<T>(acc, lp, lq, k0, k1, smem);
-  wgrad_epilogue_v2<T>(acc, a, e, r0, c0, smem);
-}
-
 // ---------------------------------------------------------------------------------------------
 // Host-side launch helpers.
 
@@ -734,6 +754,8 @@ static int launch_wgrad(const WgradArgs& a, int E, hipStream_t s) {
 }
 
 
+// 256x256 token GEMMs: the eight-wave ring kernel when K is a multiple of its 64-value step,
+// otherwise (dX GEMMs with K a multiple of 32) the four-wave five-stage kernel.
 template <typename T, int EPI, bool P_RC>
 static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   a.n_rtiles = EPI == EPI_GLU_FWD ? (int)((a.I + v2::TILE / 2 - 1) / (v2::TILE / 2))
@@ -743,14 +765,18 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   if (logical <= 0 || n_rows == 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  if constexpr (P_RC) {
-    auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, (int)logical);
-  } else {
-    auto kern = token_gemm_v4_kernel<T, EPI>;
+  if (a.K % 64 == 0) {
+    auto kern = token_gemm_v4_kernel<T, EPI, P_RC>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, (int)logical);
+  } else {
+    if constexpr (P_RC) {
+      auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, (int)logical);
+    } else {
+      return MOE_ERR_SHAPE;  // callers route K % 64 != 0 forwards to the first-generation kernel
+    }
   }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
@@ -764,10 +790,10 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
   if (logical <= 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  auto kern = a.r_gather ? (a.c_gather ? wgrad_v3_kernel<T, true, true> : wgrad_v3_kernel<T, true, false>)
-                         : (a.c_gather ? wgrad_v3_kernel<T, false, true> : wgrad_v3_kernel<T, false, false>);
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, order, E_glu,
+  auto kern = a.r_gather ? (a.c_gather ? wgrad_v4_kernel<T, true, true> : wgrad_v4_kernel<T, true, false>)
+                         : (a.c_gather ? wgrad_v4_kernel<T, false, true> : wgrad_v4_kernel<T, false, false>);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, order, E_glu,
                      (int)logical);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }

@@ -14,7 +14,7 @@
 // 32 KB slots (below). Wave w DMAs rows 32w .. 32w+31 of an operand: four global_load_lds_dwordx4,
 // each covering 8 whole 128-byte rows.
 #pragma once
-#include "moe_gemm_v2.h"
+#include "moe_gemm_v3.h"
 
 namespace moe {
 namespace v4 {
@@ -39,26 +39,118 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 __device__ __forceinline__ int wave_r() { return wave_id() & 1; }
 __device__ __forceinline__ int wave_c() { return wave_id() >> 1; }
 
-// K-contiguous operand. Lane l of wave w fills tile row R = 32w + 8i + l/8 (i < 4), physical
-// chunk l%8, i.e. logical chunk (l%8) ^ ((R >> 1) & 7) = (l%8) ^ ((4*(i&1) + l/16) & 7).
-struct DmaKc {
+// ---------------------------------------------------------------------------------------------
+// Operand loaders. Each fills one ring slot (one operand's 64-value K step, 32 KB) with four DMA
+// instructions per wave (issue) and reads MFMA operand fragments from a slot (frag): fragment t
+// (< NT_ rows-of-32 of this wave's block), slab sl (16 K values), chunk c (< CPL).
+
+// K-contiguous operand: [256 rows][128 bytes], chunk index XOR-ed by (row >> 1) & 7. Lane l of
+// wave w fills row R = 32w + 8i + l/8 (i < 4), physical chunk l%8, i.e. logical chunk
+// (l%8) ^ ((R >> 1) & 7) = (l%8) ^ ((4*(i&1) + l/16) & 7).
+struct KcLoad {
   const char* rowp[LOADS];  // this lane's rows (clamped to a valid row when outside the operand)
   int cbyte[2];             // byte offset of this lane's logical chunk for even / odd i
+  int fbase;                // fragment reads: byte offset of row rbase + (l & 31)
+  int half, sw;
 
-  __device__ __forceinline__ void init() {
+  // rbase: first operand row of this wave's fragment block.
+  __device__ __forceinline__ void init(int rbase) {
     const int l = lane_id();
     cbyte[0] = ((l & 7) ^ (l >> 4)) << 4;
     cbyte[1] = ((l & 7) ^ ((4 + (l >> 4)) & 7)) << 4;
+    fbase = (rbase + (l & 31)) * ROWB;
+    half = l >> 5;
+    sw = (l >> 1) & 7;
   }
   __device__ __forceinline__ static int row_of(int i) {
     return ((int)threadIdx.x >> 6) * 32 + i * 8 + (lane_id() >> 3);
   }
+  __device__ __forceinline__ void prime(int) {}
   template <typename T>
-  __device__ __forceinline__ void issue(char* op, int k) {
-    char* base = op + wave_id() * 32 * ROWB;
+  __device__ __forceinline__ void issue(char* slot, int k) {
+    char* base = slot + wave_id() * 32 * ROWB;
     const int kb = k * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) dma16(rowp[i] + kb + cbyte[i & 1], base + i * 8 * ROWB);
+  }
+  template <int CPL>
+  __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int c) const {
+    const int cb = (((2 * sl + half) * CPL + c) ^ sw) << 4;
+    return *(const i32x4*)(slot + fbase + t * 32 * ROWB + cb);
+  }
+};
+
+// Row-contiguous operand (element (r, k) at src + row(k) * ld + 2r, src at column r0; row(k) =
+// gather[k] or k): [64 K rows][256 r x 2 bytes], the 16-byte chunk index XOR-ed by 4 * (k & 3)
+// (the XOR applies to the whole chunk index: wave blocks of 64 columns start at odd multiples of 8).
+// Fragments are read with ds_read_b64_tr_b16, which transposes 16-bit elements across each group
+// of 16 lanes: if lane j of the group addresses 4 consecutive elements D[j][0..3], lane i receives
+// D[4q + i/4][i%4] for q = 0..3. Pointing lane 4q + p at X[k + q][r + 4p .. 4p + 3] hands lane i
+// the values X[k .. k+3][r + i], i.e. four consecutive K of one row, the MFMA operand layout; a
+// 32-lane half reads 4 K rows x 64 bytes and the XOR puts them on disjoint banks. Lane l of wave w
+// fills K row 8w + 2i + h (h = l/32), physical chunk l%32, i.e. logical chunk
+// (l%32) ^ 4*((2i + h) & 3) = columns 8c .. 8c+7. K values at or past kend read a zero block.
+constexpr int RC_ROWB = TILE * 2;  // 512 bytes per K row
+template <bool GATHER, int NFRAG>
+struct RcLoad {
+  const char* src;
+  size_t ld;
+  const int32_t* gather;
+  int kend;           // K values >= kend read zeros
+  int cbyte[2];       // column byte offsets for even / odd i (clamped inside the operand)
+  int zoff[2];        // zero-block offsets of the same chunks
+  int toff[NFRAG];    // fragment reads: byte offset of fragment t for slab 0
+  int gi[8];          // GATHER: row indices of this wave's 8 K rows of the next issue
+
+  // rbase: first column (r) of this wave's fragment block; rvalid: columns inside the operand.
+  __device__ __forceinline__ void init(int rbase, int rvalid) {
+    const int l = lane_id(), h = l >> 5;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int c = (l & 31) ^ (4 * ((2 * par + h) & 3));
+      cbyte[par] = min(8 * c, rvalid - 8) * 2;
+      zoff[par] = c * 16;
+    }
+    const int G = (l >> 4) & 1, j = l & 15, q = j >> 2, p = j & 3;
+#pragma unroll
+    for (int t = 0; t < NFRAG; ++t)
+      toff[t] = (8 * h + q) * RC_ROWB + ((((rbase >> 3) + 4 * t + 2 * G + (p >> 1)) ^ (4 * q)) * 16) +
+                8 * (p & 1);
+  }
+  __device__ __forceinline__ void fetch_rows(int k) {
+    if constexpr (GATHER) {
+      const int kw = k + wave_id() * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) gi[j] = v3::sload(gather + min(kw + j, kend - 1));
+    }
+  }
+  // Called once with the first K of the operand's first issue.
+  __device__ __forceinline__ void prime(int k) { fetch_rows(k); }
+  template <typename T>
+  __device__ __forceinline__ void issue(char* slot, int k) {
+    const int w = wave_id(), h = lane_id() >> 5;
+    static_for<0, LOADS>([&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      const int kk = k + w * 8 + 2 * I;  // K row of lanes 0-31; lanes 32-63 take kk + 1
+      int row;
+      if constexpr (GATHER) row = h ? gi[2 * I + 1] : gi[2 * I];
+      else row = kk + h;
+      const char* g = (kk + h < kend) ? src + (size_t)row * ld + cbyte[I & 1]
+                                      : (const char*)v3::g_zero_block + zoff[I & 1];
+      dma16(g, slot + w * (8 * RC_ROWB) + I * 1024);
+    });
+    fetch_rows(k + 64);
+  }
+  template <int CPL>
+  __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int) const {
+    typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s4;
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    const char* p0 = slot + toff[t] + sl * 16 * RC_ROWB;
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p0);
+    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * RC_ROWB));
+    typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i2;
+    const i2 x = __builtin_bit_cast(i2, lo), y = __builtin_bit_cast(i2, hi);
+    return i32x4{x[0], x[1], y[0], y[1]};
   }
 };
 
@@ -67,16 +159,17 @@ struct DmaKc {
 // waits for every outstanding global load of the wave, so a K loop that synchronises with it
 // drains its whole load queue once per step, and the queue depth never exceeds one step (about
 // 45 GB/s per CU delivered). Here the LDS holds a ring of NSLOT = 5 slots of 32 KB, each one
-// operand's K step (256 rows x 128 bytes), filled in the order P0 Q0 P1 Q1 P2 ...; a slot is
-// refilled as soon as the step that read it is over, so 1-3 slots (32-96 KB per CU) stay in
-// flight across every step boundary. Waits are per wave and partial (s_waitcnt vmcnt(N), loads
-// retire in issue order); the block barrier is a bare s_barrier after the wave's own LDS reads
-// have returned (s_waitcnt lgkmcnt(0)), which orders (a) every wave's DMA of the slots about to be
-// read before any wave reads them and (b) every wave's reads of the slots about to be refilled
-// before any wave's DMA into them.
+// operand's K step, filled in the order P0 Q0 P1 Q1 P2 ...; a slot is refilled as soon as the step
+// that read it is over, so 1-3 slots (32-96 KB per CU) stay in flight across every step boundary.
+// Waits are per wave and partial (s_waitcnt vmcnt(N), loads retire in issue order); the block
+// barrier is a bare s_barrier after the wave's own LDS reads have returned (s_waitcnt
+// lgkmcnt(0)), which orders (a) every wave's DMA of the slots about to be read before any wave
+// reads them and (b) every wave's reads of the slots about to be refilled before any wave's DMA
+// into them.
 constexpr int NSLOT = 5;
 constexpr int SLOTB = OPB;                 // 32 KB
 constexpr int RING_LDSB = NSLOT * SLOTB;   // 160 KB
+static_assert(64 * RC_ROWB == SLOTB, "both layouts fill one slot");
 
 __device__ __forceinline__ void bare_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -89,27 +182,26 @@ __device__ __forceinline__ void wait_slots(int n) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// K loop over the ring. Step s reads P_s from slot (2s) % NSLOT and Q_s from (2s+1) % NSLOT. The
-// synchronisation sits before the last slab of each step: wait for this wave's loads of step s+1,
-// barrier, refill the two slots step s has finished reading (with Q_{s+2} and P_{s+3}), read the
-// first slab of step s+1, then run the last slab's MFMAs, whose operands were read before the
-// barrier and which cover the latency of those reads.
-template <typename T>
-__device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], DmaKc& lp, DmaKc& lq, int k0,
-                                              int k1, char* smem) {
+// K loop over the ring: acc[ti][tj] += P(wave block) . Q(wave block) over K in [k0, k1). Step s
+// reads P_s from slot (2s) % NSLOT and Q_s from (2s+1) % NSLOT. The synchronisation sits before
+// the last slab of each step: wait for this wave's loads of step s+1, barrier, refill the two
+// slots step s has finished reading (with Q_{s+2} and P_{s+3}), read the first slab of step s+1,
+// then run the last slab's MFMAs, whose operands were read before the barrier and which cover the
+// latency of those reads.
+template <typename T, class LP, class LQ>
+__device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ& lq, int k0, int k1,
+                                              char* smem) {
   constexpr int KS = v2::bk<T>();
   constexpr int CPL = Mfma<T>::CPL;
   constexpr int SLABS = ROWB / (32 * CPL);
   static_assert(SLABS >= 2, "the mid-step barrier needs at least two slabs per step");
   const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;
-  const int lane = lane_id();
-  const int pbase = (wave_r() * WP + (lane & 31)) * ROWB;
-  const int qbase = (wave_c() * WQ + (lane & 31)) * ROWB;
-  const int half = lane >> 5, sw = (lane >> 1) & 7;
   const int nslab = 2 * nk;  // ring loads of the whole loop: P_j is load 2j, Q_j is load 2j+1
 
   // Prologue: loads 0..NSLOT-1 (P0 Q0 P1 Q1 P2) into slots 0..4.
+  lp.prime(k0);
+  lq.prime(k0);
   int issued = 0;
   for (; issued < NSLOT && issued < nslab; ++issued) {
     char* slot = smem + issued * SLOTB;
@@ -124,18 +216,17 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], DmaKc& lp, 
   auto load = [&](int f, const char* ps, const char* qs, int sl) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      const int cb = (((2 * sl + half) * CPL + c) ^ sw) << 4;
 #pragma unroll
-      for (int t = 0; t < TI; ++t) a[f][t][c] = *(const i32x4*)(ps + t * 32 * ROWB + cb);
+      for (int t = 0; t < TI; ++t) a[f][t][c] = lp.template frag<CPL>(ps, t, sl, c);
 #pragma unroll
-      for (int t = 0; t < TJ; ++t) b[f][t][c] = *(const i32x4*)(qs + t * 32 * ROWB + cb);
+      for (int t = 0; t < TJ; ++t) b[f][t][c] = lq.template frag<CPL>(qs, t, sl, c);
     }
   };
   int sp = 0, sq = 1;  // slots of P_s, Q_s
-  load(0, smem + sp * SLOTB + pbase, smem + sq * SLOTB + qbase, 0);
+  load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
   for (int s = 0; s < nk; ++s) {
-    const char* ps = smem + sp * SLOTB + pbase;
-    const char* qs = smem + sq * SLOTB + qbase;
+    const char* ps = smem + sp * SLOTB;
+    const char* qs = smem + sq * SLOTB;
     const int np = sp + 2 >= NSLOT ? sp + 2 - NSLOT : sp + 2;
     const int nq = sq + 2 >= NSLOT ? sq + 2 - NSLOT : sq + 2;
 #pragma unroll
@@ -155,7 +246,7 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], DmaKc& lp, 
           lp.template issue<T>(smem + sq * SLOTB, k0 + (s + 3) * KS);
           ++issued;
         }
-        load(f ^ 1, smem + np * SLOTB + pbase, smem + nq * SLOTB + qbase, 0);
+        load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
