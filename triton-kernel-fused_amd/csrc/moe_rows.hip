@@ -2,9 +2,10 @@
 // un-permute of the input gradient, and the row-wise PolyGLU activation (BatchedGLU) forward and
 // backward for every activation code.
 //
-// Combine and un-permute are gathers, not scatters: one wave owns one token and sums its k routed
-// rows in slot order in fp32, so results are deterministic and need no atomics (the reference
-// scatters with fp32 atomics or index_add_, /root/reference/kernels/sm75/moe.py:673-682,593-595).
+// Combine and un-permute are gathers, not scatters: one wave owns one token's 64*V-column chunk
+// and sums its k routed rows in slot order in fp32, so results are deterministic and need no
+// atomics (the reference scatters with fp32 atomics or index_add_,
+// /root/reference/kernels/sm75/moe.py:673-682,593-595).
 #include "moe_common.h"
 
 namespace moe {
@@ -82,35 +83,75 @@ __device__ __forceinline__ int slot_kind(int64_t e, const int32_t* codes, int E_
   return c == 3 ? 1 : 2;
 }
 
+// Per-token gathers (combine forward, un-permute backward). One wave owns cpw consecutive
+// 64*V-column chunks of one token; for each chunk the k routed rows are loaded BATCH at a time
+// (the token's routing reads are wave-uniform) and summed in slot order in fp32:
+//   acc = sum_j g_j * row_j,  row_j = rows[f2s[t,j]] for a GLU expert (g_j = gate if GATE_GLU,
+//   else 1) or self[t] for an Identity expert (g_j = gate); Zero experts and invalid ids add
+//   nothing.
+template <typename T, bool GATE_GLU, int BATCH>
+__device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T* __restrict__ self,
+                                             int64_t self_ld, const T* __restrict__ wt,
+                                             const int64_t* __restrict__ idx,
+                                             const int32_t* __restrict__ codes, int E_glu,
+                                             int E_all, const int32_t* __restrict__ f2s,
+                                             int64_t N, int k, int H, T* __restrict__ out,
+                                             int cpw) {
+  constexpr int V = Vec8<T>::N;
+  const int nchunk = (H + 64 * V - 1) / (64 * V);
+  const int ngroup = (nchunk + cpw - 1) / cpw;  // waves per token
+  const int64_t wv = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
+  if (wv >= N * ngroup) return;
+  const int64_t t = wv / ngroup;
+  const int lane = threadIdx.x & 63;
+  const int cg = (int)(wv % ngroup) * cpw;
+  for (int ci = cg; ci < cg + cpw && ci < nchunk; ++ci) {
+    const int c = ci * 64 * V + lane * V;
+    const bool col_ok = c < H;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int j0 = 0; j0 < k; j0 += BATCH) {
+      float v[BATCH][V], w[BATCH];
+#pragma unroll
+      for (int jj = 0; jj < BATCH; ++jj) {
+        const int j = j0 + jj;
+        bool used = false;
+        if (j < k) {
+          const int64_t f = t * k + j;
+          const int pos = f2s[f];
+          const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+          if (kind != 2 && col_ok) {
+            used = true;
+            w[jj] = (kind == 0 && !GATE_GLU) ? 1.f : to_f32(wt[f]);
+            if (kind == 0) Vec8<T>::ld(rows + (size_t)pos * H + c, v[jj]);
+            else Vec8<T>::ld(self + (size_t)t * self_ld + c, v[jj]);
+          }
+        }
+        if (!used) {  // skipped slot: contributes nothing (not even 0 * inf)
+          w[jj] = 0.f;
+#pragma unroll
+          for (int i = 0; i < V; ++i) v[jj][i] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < BATCH; ++jj)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += w[jj] * v[jj][i];
+    }
+    if (col_ok) Vec8<T>::st(out + (size_t)t * H + c, acc);
+  }
+}
+
 // out[t] = sum_j w[t,j] * row(t,j)
-template <typename T>
+template <typename T, int BATCH>
 __global__ void __launch_bounds__(ROW_THREADS)
 combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
                    const T* __restrict__ wt, const int64_t* __restrict__ idx,
                    const int32_t* __restrict__ codes, int E_glu, int E_all,
-                   const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out) {
-  constexpr int V = Vec8<T>::N;
-  const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
-  if (t >= N) return;
-  const int lane = threadIdx.x & 63;
-  for (int c = lane * V; c < H; c += 64 * V) {
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int j = 0; j < k; ++j) {
-      const int64_t f = t * k + j;
-      const int pos = f2s[f];
-      const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
-      if (kind == 2) continue;
-      const float w = to_f32(wt[f]);
-      float v[V];
-      if (kind == 0) Vec8<T>::ld(eo + (size_t)pos * H + c, v);
-      else Vec8<T>::ld(hidden + (size_t)t * H + c, v);
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += w * v[i];
-    }
-    Vec8<T>::st(out + (size_t)t * H + c, acc);
-  }
+                   const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out,
+                   int cpw) {
+  token_gather<T, true, BATCH>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out, cpw);
 }
 
 // Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
@@ -153,40 +194,15 @@ combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict_
 }
 
 // grad_x[t] = sum_j (GLU: grad_xs[pos]; Identity: w*go[t]; Zero: 0)
-template <typename T>
+template <typename T, int BATCH>
 __global__ void __launch_bounds__(ROW_THREADS)
 unpermute_bwd_kernel(const T* __restrict__ gxs, const T* __restrict__ go, int64_t go_ld,
                      const T* __restrict__ wt, const int64_t* __restrict__ idx,
                      const int32_t* __restrict__ codes, int E_glu, int E_all,
                      const int32_t* __restrict__ f2s, int64_t N, int k, int H,
-                     T* __restrict__ gx) {
-  constexpr int V = Vec8<T>::N;
-  const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
-  if (t >= N) return;
-  const int lane = threadIdx.x & 63;
-  for (int c = lane * V; c < H; c += 64 * V) {
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int j = 0; j < k; ++j) {
-      const int64_t f = t * k + j;
-      const int pos = f2s[f];
-      const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
-      if (kind == 2) continue;
-      float v[V];
-      if (kind == 0) {
-        Vec8<T>::ld(gxs + (size_t)pos * H + c, v);
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] += v[i];
-      } else {
-        const float w = to_f32(wt[f]);
-        Vec8<T>::ld(go + (size_t)t * go_ld + c, v);
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] += w * v[i];
-      }
-    }
-    Vec8<T>::st(gx + (size_t)t * H + c, acc);
-  }
+                     T* __restrict__ gx, int cpw) {
+  // GLU expert rows of grad_xs already carry the gate weight; Identity slots add w * grad_out.
+  token_gather<T, false, BATCH>(gxs, go, go_ld, wt, idx, codes, E_glu, E_all, f2s, N, k, H, gx, cpw);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -340,6 +356,20 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
       hipLaunchKernelGGL(KERNEL<T_>, GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
     }                                                              \
   } while (0)
+// The same for kernels with a second (integer) template parameter B.
+#define MOE_BY_DTYPE_B(dtype, KERNEL, B, GRID, BLOCK, STREAM, ...)      \
+  do {                                                             \
+    if ((dtype) == MOE_DT_BF16) {                                  \
+      typedef bf16 T_;                                             \
+      hipLaunchKernelGGL((KERNEL<T_, B>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    } else if ((dtype) == MOE_DT_F16) {                            \
+      typedef f16 T_;                                              \
+      hipLaunchKernelGGL((KERNEL<T_, B>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    } else {                                                       \
+      typedef float T_;                                            \
+      hipLaunchKernelGGL((KERNEL<T_, B>), GRID, BLOCK, 0, STREAM, __VA_ARGS__); \
+    }                                                              \
+  } while (0)
 
 static int check_rows(int dtype, int64_t n, int top_k, int64_t H, int n_experts, int E_glu) {
   if (dtype < 0 || dtype > 2) return MOE_ERR_DTYPE;
@@ -351,6 +381,19 @@ static int check_rows(int dtype, int64_t n, int top_k, int64_t H, int n_experts,
 }
 
 static unsigned row_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
+
+// Waves per token for the per-token gathers (combine, un-permute) and the 64*vec-column chunks
+// each wave sums (*cpw): one chunk per wave while that leaves fewer than ~16K waves (decode
+// batches; the rows are then loaded 8 at a time for memory-level parallelism), else whole-token
+// waves loading one row at a time (measured faster when the grid alone fills the GPU).
+static int64_t token_col_waves(int64_t n_tokens, int64_t H, int vec, int* cpw) {
+  const int64_t nchunk = (H + 64 * vec - 1) / (64 * vec);
+  const int64_t target = 16384;
+  int64_t c = n_tokens >= target ? nchunk : (n_tokens * nchunk + target - 1) / target;
+  c = c < 1 ? 1 : (c > nchunk ? nchunk : c);
+  *cpw = (int)c;
+  return (nchunk + c - 1) / c;
+}
 
 extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
                                const void* top_k_weights, const int64_t* top_k_indices,
@@ -364,11 +407,19 @@ extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
       (E_glu > 0 && !eo))
     return MOE_ERR_SHAPE;
   if (!al16(hidden) || !al16(out) || (eo && !al16(eo))) return MOE_ERR_ALIGN;
-  if (row_grid(n_tokens) >= (1u << 31)) return MOE_ERR_SHAPE;
+  int cpw;
+  const int64_t col_waves = token_col_waves(n_tokens, H, vec_of(dtype), &cpw);
+  if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  MOE_BY_DTYPE(dtype, combine_fwd_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
-               (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-               act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
+  const dim3 grid(row_grid(n_tokens * col_waves));
+  if (col_waves == 1)
+    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 1, grid, dim3(ROW_THREADS), s,
+                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out, cpw);
+  else
+    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 8, grid, dim3(ROW_THREADS), s,
+                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out, cpw);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -410,10 +461,20 @@ extern "C" int moe_unpermute_bwd(int dtype, const void* grad_xs, const void* gra
   if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
   if (!al16(grad_out) || !al16(grad_x_out) || (grad_xs && !al16(grad_xs))) return MOE_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  MOE_BY_DTYPE(dtype, unpermute_bwd_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
-               (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
-               top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
-               (int)H, (T_*)grad_x_out);
+  int cpw;
+  const int64_t col_waves = token_col_waves(n_tokens, H, vec_of(dtype), &cpw);
+  if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
+  const dim3 grid(row_grid(n_tokens * col_waves));
+  if (col_waves == 1)
+    MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 1, grid, dim3(ROW_THREADS), s,
+                   (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
+                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+                   (int)H, (T_*)grad_x_out, cpw);
+  else
+    MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 8, grid, dim3(ROW_THREADS), s,
+                   (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
+                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+                   (int)H, (T_*)grad_x_out, cpw);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
