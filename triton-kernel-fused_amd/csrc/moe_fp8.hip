@@ -2,14 +2,14 @@
 // re-quantisation of the intermediate, grouped down GEMM with scales.
 //
 // Operands are OCP e4m3fn with fp32 scales: activations per token, weights per output channel,
-// the intermediate per routed row (absmax / 448). The GEMMs run the 256x256 DMA-fed pipeline of
-// moe_gemm_v2.h on v_mfma_scale_f32_32x32x64_f8f6f4 with neutral E8M0 scales (the plain fp8
-// product); the per-token and per-channel scales factor out of the K sum and are applied in the
+// the intermediate per routed row (absmax / 448). The GEMMs run the eight-wave 256x256 ring
+// pipeline of moe_gemm_v4.h on v_mfma_scale_f32_32x32x64_f8f6f4 with neutral E8M0 scales (the
+// plain fp8 product); the per-token and per-channel scales factor out of the K sum and are applied in the
 // epilogue: y[m, n] = (sum_k xq[m,k] wq[n,k]) * sx[m] * sw[n].
 // The gate/up epilogue cannot quantise the intermediate itself (a row's absmax spans every
 // column tile), so it stores SiLU(gate)*up in bf16 and a row kernel quantises it.
 #include "moe_gemm_common.h"
-#include "moe_gemm_v2.h"
+#include "moe_gemm_v4.h"
 
 namespace moe {
 
@@ -30,16 +30,15 @@ struct Fp8Args {
 };
 
 template <bool GLU>
-__global__ void __launch_bounds__(v2::NT, 1)
+__global__ void __launch_bounds__(v4::NT, 1)
 fp8_gemm_kernel(Fp8Args a, int n_logical) {
-  using C = Cfg<fp8e4m3, v2::TILE, v2::TILE, 2, 2>;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ int s_pref[MAX_GLU_EXPERTS + 1];
-  __shared__ int s_wsum[v2::NT / 64];
-
-  tile_prefix<v2::NT>(a.offsets, a.E_glu, v2::TILE, s_pref, s_wsum);
-  const int lid = v2::xcd_logical((int)blockIdx.x, (int)gridDim.x);
+  using C = Cfg<fp8e4m3, v4::TILE, v4::TILE, 2, 2>;  // GLU row interleave per 128-row P half
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  const int lid = v4::xcd_logical((int)blockIdx.x, (int)gridDim.x);
   if (lid >= n_logical) return;
+  // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
+  int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
+  tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
   const int mt = lid / a.n_rtiles;
   const int rt = lid % a.n_rtiles;
   if (mt >= s_pref[a.E_glu]) return;
@@ -49,60 +48,63 @@ fp8_gemm_kernel(Fp8Args a, int n_logical) {
     if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
   }
   const int e = lo;
-  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v2::TILE;
+  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v4::TILE;
   const int m_end = a.offsets[e + 1];
   const fp8e4m3* Pe = a.P + (size_t)e * a.p_e;
+  const int wr = v4::wave_r(), wc = v4::wave_c();
 
-  v2::DmaKc lq;
-  lq.init();
+  v4::KcLoad lq;
+  lq.init(wc * v4::WQ);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int m = m0 + v2::DmaKc::row_of(i);
+  for (int i = 0; i < v4::LOADS; ++i) {
+    int m = m0 + v4::KcLoad::row_of(i);
     if (m >= m_end) m = m0;
     const int qr = a.q_gather ? a.q_gather[m] : m;
     lq.rowp[i] = (const char*)(a.Q + (size_t)qr * a.q_ld);
   }
-  v2::DmaKc lp;
-  lp.init();
+  v4::KcLoad lp;
+  lp.init(wr * v4::WP);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = v2::DmaKc::row_of(i);
+  for (int i = 0; i < v4::LOADS; ++i) {
+    const int rr = v4::KcLoad::row_of(i);
     bool ok;
     int prow;
     if (GLU) {
       prow = glu_prow<C>(rr, rt, a.I, ok);
     } else {
-      prow = rt * v2::TILE + rr;
+      prow = rt * v4::TILE + rr;
       ok = prow < a.R;
     }
     lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
   }
 
-  f32x16 acc[v2::TN][v2::TN];
+  f32x16 acc[v4::TI][v4::TJ];
 #pragma unroll
-  for (int ti = 0; ti < v2::TN; ++ti)
+  for (int ti = 0; ti < v4::TI; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < v2::TN; ++tj)
+    for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-  v2::mainloop<fp8e4m3>(acc, lp, lq, 0, a.K, smem);
+  __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+  v4::mainloop_ring<fp8e4m3>(acc, lp, lq, 0, a.K, smem);
 
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wr = wid / C::WC, wc = wid % C::WC;
+  // Epilogue from registers: lane (l & 31) of fragment tj is token row m; each lane holds four
+  // consecutive output channels per 8-channel group g (half h of the lane).
+  const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
   const float* ps = a.p_scale + (size_t)e * a.ps_e;
-  static_for<0, C::TJ>([&](auto tj_c) {
+  static_for<0, v4::TJ>([&](auto tj_c) {
     constexpr int tj = decltype(tj_c)::value;
-    const int m = m0 + wc * C::WTC + tj * 32 + (lane & 31);
+    const int m = m0 + wc * v4::WQ + tj * 32 + (lane & 31);
     if (m >= m_end) return;
     const float qs = a.q_scale[a.q_gather ? a.q_gather[m] : m];
     if constexpr (GLU) {
       bf16* it = a.out + (size_t)m * a.I;
 #pragma unroll
-      for (int ti = 0; ti < C::TI / 2; ++ti)
+      for (int ti = 0; ti < v4::TI / 2; ++ti)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int ch = rt * (C::BR / 2) + wr * (C::WTR / 2) + ti * 32 + 8 * g + 4 * h;
+          const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + ti * 32 + 8 * g + 4 * h;
           if (ch >= a.I) continue;
           const f32x4 sg = *(const f32x4*)(ps + ch);
           const f32x4 su = *(const f32x4*)(ps + a.I + ch);
@@ -110,7 +112,7 @@ fp8_gemm_kernel(Fp8Args a, int n_logical) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const float gv = acc[ti][tj][4 * g + j] * qs * sg[j];
-            const float uv = acc[ti + C::TI / 2][tj][4 * g + j] * qs * su[j];
+            const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qs * su[j];
             iv[j] = silu(gv) * uv;
           }
           Store4<bf16>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
@@ -118,10 +120,10 @@ fp8_gemm_kernel(Fp8Args a, int n_logical) {
     } else {
       bf16* o = a.out + (size_t)m * a.out_ld;
 #pragma unroll
-      for (int ti = 0; ti < C::TI; ++ti)
+      for (int ti = 0; ti < v4::TI; ++ti)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int r = rt * C::BR + wr * C::WTR + ti * 32 + 8 * g + 4 * h;
+          const int r = rt * v4::TILE + wr * v4::WP + ti * 32 + 8 * g + 4 * h;
           if (r >= a.R) continue;
           const f32x4 sr = *(const f32x4*)(ps + r);
           Store4<bf16>::st(o + r, acc[ti][tj][4 * g] * qs * sr[0], acc[ti][tj][4 * g + 1] * qs * sr[1],
@@ -181,8 +183,8 @@ static int launch_fp8(Fp8Args a, int64_t n_rows, hipStream_t s) {
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   auto kern = fp8_gemm_kernel<GLU>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v2::LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v2::NT), v2::LDSB, s, a, (int)logical);
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, (int)logical);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 

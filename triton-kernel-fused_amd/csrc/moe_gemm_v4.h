@@ -212,7 +212,11 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
   wait_slots(issued - 2);
   bare_barrier();
 
-  i32x4 a[2][TI][CPL], b[2][TJ][CPL];
+  // Operand fragments are double-buffered in registers (slab sl+1 read while slab sl's MFMAs run)
+  // for 16-bit operands; fp8 fragments are twice as large, so they are single-buffered (the
+  // other wave of the SIMD covers the read latency).
+  constexpr int FB = CPL > 1 ? 1 : 2;
+  i32x4 a[FB][TI][CPL], b[FB][TJ][CPL];
   auto load = [&](int f, const char* ps, const char* qs, int sl) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -222,8 +226,28 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
       for (int t = 0; t < TJ; ++t) b[f][t][c] = lq.template frag<CPL>(qs, t, sl, c);
     }
   };
+  auto mfmas = [&](int f) {
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
+  };
+  // Mid-step synchronisation: step s+1 landed (this wave's loads, then the barrier), and the two
+  // slots of step s are refilled with Q_{s+2} (slot sp) and P_{s+3} (slot sq).
+  auto sync_refill = [&](int s, int sp, int sq) {
+    wait_slots(issued - (2 * s + 4));
+    bare_barrier();
+    if (issued < nslab) {
+      lq.template issue<T>(smem + sp * SLOTB, k0 + (s + 2) * KS);
+      ++issued;
+    }
+    if (issued < nslab) {
+      lp.template issue<T>(smem + sq * SLOTB, k0 + (s + 3) * KS);
+      ++issued;
+    }
+  };
   int sp = 0, sq = 1;  // slots of P_s, Q_s
-  load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
+  if constexpr (FB == 2) load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
   for (int s = 0; s < nk; ++s) {
     const char* ps = smem + sp * SLOTB;
     const char* qs = smem + sq * SLOTB;
@@ -231,28 +255,22 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
     const int nq = sq + 2 >= NSLOT ? sq + 2 - NSLOT : sq + 2;
 #pragma unroll
     for (int sl = 0; sl < SLABS; ++sl) {
-      const int f = sl & 1;
-      if (sl + 1 < SLABS) {
-        load(f ^ 1, ps, qs, sl + 1);
-      } else if (s + 1 < nk) {
-        wait_slots(issued - (2 * s + 4));
-        bare_barrier();
-        // Slot sp (P_s) takes load 2s+5 = Q_{s+2}; slot sq (Q_s) takes load 2s+6 = P_{s+3}.
-        if (issued < nslab) {
-          lq.template issue<T>(smem + sp * SLOTB, k0 + (s + 2) * KS);
-          ++issued;
+      if constexpr (FB == 2) {
+        const int f = sl & 1;
+        if (sl + 1 < SLABS) {
+          load(f ^ 1, ps, qs, sl + 1);
+        } else if (s + 1 < nk) {
+          sync_refill(s, sp, sq);
+          load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
         }
-        if (issued < nslab) {
-          lp.template issue<T>(smem + sq * SLOTB, k0 + (s + 3) * KS);
-          ++issued;
-        }
-        load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(f);
+      } else {
+        load(0, ps, qs, sl);
+        if (sl + 1 == SLABS && s + 1 < nk) sync_refill(s, sp, sq);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
       __builtin_amdgcn_sched_barrier(0);
     }
     sp = np;
