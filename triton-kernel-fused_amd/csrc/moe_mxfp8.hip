@@ -48,6 +48,10 @@ __device__ __forceinline__ i32x4 dequant8(unsigned lo, unsigned hi, float sc) {
 
 // KSPLIT waves share one row tile and split its K range (partials summed through LDS); the
 // block's 4/KSPLIT tiles are consecutive row tiles. a.n_rtiles counts row tiles.
+// LDS per block: staged token rows (up to MX_XLDS bytes), reused for the K-split partial sums.
+constexpr size_t MX_XLDS = 80 * 1024;
+static_assert(MX_XLDS >= sizeof(f32x16) * 4 * 2 * 64, "partial sums fit");
+
 template <bool GLU, int KSPLIT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
@@ -56,7 +60,8 @@ mx_gemm_kernel(MxArgs a) {
   const int e = (int)blockIdx.x / nb;
   const int m_begin = a.offsets[e], m_end = a.offsets[e + 1];
   if (m_begin >= m_end) return;
-  __shared__ f32x16 red[4][2][64];  // partial accumulators
+  extern __shared__ __attribute__((aligned(16))) char xlds[];  // token rows, then partial sums
+  f32x16 (*red)[2][64] = (f32x16 (*)[2][64])xlds;
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int w = wv % KSPLIT;                                      // K part of this wave
@@ -97,55 +102,91 @@ mx_gemm_kernel(MxArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) { acc0[v] = 0.f; acc1[v] = 0.f; }
 
+    // When this block's tokens fit in LDS (a decode batch gives an expert a handful), they are
+    // staged once and every wave reads its token fragments from LDS instead of re-reading 8 KB
+    // from L2 per 128-byte weight chunk; padding lanes read the last real token's row.
+    const int nt = min(32, m_end - mb);
+    const bool x_lds = (size_t)nt * a.K * sizeof(bf16) <= MX_XLDS;
+    if (x_lds) {
+      const int units = a.K / 8;  // 16-byte units per token row
+      for (int u = threadIdx.x; u < nt * units; u += blockDim.x) {
+        const int tt = u / units, o = u % units;
+        const int gm = mb + tt;
+        const int gr = a.x_gather ? a.x_gather[gm] : gm;
+        *(i32x4*)(xlds + ((size_t)tt * a.K + 8 * o) * sizeof(bf16)) =
+            ldg16(a.X + (size_t)gr * a.x_ld + 8 * o);
+      }
+      __syncthreads();
+    }
+    const char* xl = xlds + (size_t)min(r, nt - 1) * a.K * sizeof(bf16);
+
     // Software pipeline over two register buffers (no copies): everything chunk c+1 needs (token
     // fragments, weights, scales) is issued before chunk c computes. Vector loads retire in issue
     // order, so chunk c waits only for loads issued an iteration earlier. The prefetch is
     // unconditional (the last one re-reads a valid chunk) so every path has the same count of
     // loads in flight and the compiler's waits stay partial.
-    struct Buf {
-      i32x4 x[8];
-      uint4 a[4], b[4];
-      unsigned short sa, sb;
-    };
-    Buf p0, p1;
-    auto fetch = [&](int c, Buf& f) {
-      const int kb = c * 128 + h * 64;
+    auto kloop = [&](auto xl_c) {
+      constexpr bool XL = decltype(xl_c)::value;
+      struct Buf {
+        i32x4 x[XL ? 1 : 8];
+        uint4 a[4], b[4];
+        unsigned short sa, sb;
+      };
+      Buf p0, p1;
+      auto fetch = [&](int c, Buf& f) {
+        const int kb = c * 128 + h * 64;
+        if constexpr (!XL) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) f.x[j] = ldg16(xrow + kb + 8 * j);
+          for (int j = 0; j < 8; ++j) f.x[j] = ldg16(xrow + kb + 8 * j);
+        }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f.a[i] = *(const uint4*)(w0 + kb + 16 * i);
-        f.b[i] = *(const uint4*)(w1 + kb + 16 * i);
-      }
-      f.sa = *(const unsigned short*)(s0 + kb / 32);
-      f.sb = *(const unsigned short*)(s1 + kb / 32);
-      __builtin_amdgcn_sched_barrier(0);  // issue the whole batch before the compute that follows
-    };
-    auto compute = [&](const Buf& f) {
-      const float sa0 = e8m0_to_f32(f.sa & 0xff), sa1 = e8m0_to_f32(f.sa >> 8);
-      const float sb0 = e8m0_to_f32(f.sb & 0xff), sb1 = e8m0_to_f32(f.sb >> 8);
+        for (int i = 0; i < 4; ++i) {
+          f.a[i] = *(const uint4*)(w0 + kb + 16 * i);
+          f.b[i] = *(const uint4*)(w1 + kb + 16 * i);
+        }
+        f.sa = *(const unsigned short*)(s0 + kb / 32);
+        f.sb = *(const unsigned short*)(s1 + kb / 32);
+        __builtin_amdgcn_sched_barrier(0);  // issue the whole batch before the compute that follows
+      };
+      auto compute = [&](const Buf& f, int c) {
+        i32x4 xv[8];
+        if constexpr (XL) {
+          const int kb = c * 128 + h * 64;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint4 ua = f.a[j >> 1], ub = f.b[j >> 1];
-        const i32x4 av = (j & 1) ? dequant8(ua.z, ua.w, j < 4 ? sa0 : sa1)
-                                 : dequant8(ua.x, ua.y, j < 4 ? sa0 : sa1);
-        const i32x4 bv = (j & 1) ? dequant8(ub.z, ub.w, j < 4 ? sb0 : sb1)
-                                 : dequant8(ub.x, ub.y, j < 4 ? sb0 : sb1);
-        Mfma<bf16>::step(acc0, av, f.x[j]);
-        Mfma<bf16>::step(acc1, bv, f.x[j]);
+          for (int j = 0; j < 8; ++j) xv[j] = *(const i32x4*)(xl + (kb + 8 * j) * sizeof(bf16));
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xv[j] = f.x[j];
+        }
+        const float sa0 = e8m0_to_f32(f.sa & 0xff), sa1 = e8m0_to_f32(f.sa >> 8);
+        const float sb0 = e8m0_to_f32(f.sb & 0xff), sb1 = e8m0_to_f32(f.sb >> 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint4 ua = f.a[j >> 1], ub = f.b[j >> 1];
+          const i32x4 av = (j & 1) ? dequant8(ua.z, ua.w, j < 4 ? sa0 : sa1)
+                                   : dequant8(ua.x, ua.y, j < 4 ? sa0 : sa1);
+          const i32x4 bv = (j & 1) ? dequant8(ub.z, ub.w, j < 4 ? sb0 : sb1)
+                                   : dequant8(ub.x, ub.y, j < 4 ? sb0 : sb1);
+          Mfma<bf16>::step(acc0, av, xv[j]);
+          Mfma<bf16>::step(acc1, bv, xv[j]);
+        }
+      };
+      const int c_last = c_end - 1;
+      if (c_begin <= c_last) {
+        fetch(c_begin, p0);
+        for (int c = c_begin; c <= c_last; c += 2) {
+          fetch(min(c + 1, c_last), p1);
+          compute(p0, c);
+          if (c + 1 > c_last) break;
+          fetch(min(c + 2, c_last), p0);
+          compute(p1, c + 1);
+        }
       }
     };
-    const int c_last = c_end - 1;
-    if (c_begin <= c_last) {
-      fetch(c_begin, p0);
-      for (int c = c_begin; c <= c_last; c += 2) {
-        fetch(min(c + 1, c_last), p1);
-        compute(p0);
-        if (c + 1 > c_last) break;
-        fetch(min(c + 2, c_last), p0);
-        compute(p1);
-      }
-    }
+    if (x_lds) kloop(std::true_type{});
+    else kloop(std::false_type{});
+    // The partial-sum exchange below reuses the LDS that held the tokens.
+    if (KSPLIT > 1 && x_lds) __syncthreads();
 
     if (KSPLIT > 1) {
       if (w > 0) {
@@ -208,9 +249,13 @@ template <bool GLU>
 static bool launch_mx(const MxArgs& a, int E, int ksplit, hipStream_t s) {
   const int tpb = 4 / ksplit;
   const unsigned grid = (unsigned)(E * ((a.n_rtiles + tpb - 1) / tpb));
-  if (ksplit == 1) hipLaunchKernelGGL((mx_gemm_kernel<GLU, 1>), dim3(grid), dim3(256), 0, s, a);
-  else if (ksplit == 2) hipLaunchKernelGGL((mx_gemm_kernel<GLU, 2>), dim3(grid), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((mx_gemm_kernel<GLU, 4>), dim3(grid), dim3(256), 0, s, a);
+  auto go = [&](auto kern) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)MX_XLDS);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), MX_XLDS, s, a);
+  };
+  if (ksplit == 1) go(mx_gemm_kernel<GLU, 1>);
+  else if (ksplit == 2) go(mx_gemm_kernel<GLU, 2>);
+  else go(mx_gemm_kernel<GLU, 4>);
   return hipGetLastError() == hipSuccess;
 }
 
