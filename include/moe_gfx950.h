@@ -180,7 +180,8 @@ int moe_rowquant_fp8(const void* x, int64_t n_rows, int64_t K, void* q, float* s
 /* MXFP8-weight forward for decode batches (no counterpart in the reference).
  * hidden (N,H) bf16; w13_q (E,2I,H) e4m3 + w13_scale (E,2I,H/32) E8M0 bytes; w2_q (E,H,I) e4m3 +
  * w2_scale (E,H,I/32) E8M0 (value 2^(s-127), OCP MX). Writes inter (M,I) bf16 and eo (M,H) bf16;
- * moe_combine_fwd (bf16) makes the output. H and I must be multiples of 512. */
+ * moe_combine_fwd (bf16) makes the output. H and I must be multiples of 512 and at most 32256;
+ * the scale tensors 4-byte aligned. */
 int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, const void* w13_q,
                   const void* w13_scale, const void* w2_q, const void* w2_scale, int E, int64_t I,
                   const int32_t* offsets, const int32_t* sorted_token, int64_t n_rows, void* inter,

@@ -12,7 +12,7 @@
 // (token rows read from L2: decode batches are small). The four partial accumulators are summed
 // through LDS; the gate/up kernel applies SwiGLU and writes the bf16 intermediate, the down
 // kernel writes the expert outputs, and the gate-weighted combine (moe_combine_fwd) finishes.
-#include "moe_common.h"
+#include "moe_gemm_common.h"
 
 namespace moe {
 
@@ -46,67 +46,91 @@ __device__ __forceinline__ i32x4 dequant8(unsigned lo, unsigned hi, float sc) {
                __builtin_bit_cast(int, d)};
 }
 
-// KSPLIT waves share one row tile and split its K range (partials summed through LDS); the
-// block's 4/KSPLIT tiles are consecutive row tiles. a.n_rtiles counts row tiles.
-// LDS per block: staged token rows (up to MX_XLDS bytes), reused for the K-split partial sums.
-constexpr size_t MX_XLDS = 80 * 1024;
-static_assert(MX_XLDS >= sizeof(f32x16) * 4 * 2 * 64, "partial sums fit");
+// LDS per block (two blocks per CU): the E8M0 scale table of the block's 64 rows, then the
+// staged token rows, whose space the K-split partial sums reuse after the K loop.
+constexpr int MX_LDS = 80 * 1024;
+constexpr int MX_WAVES = 4;       // waves per block; they split K
+constexpr int MX_ROWS = 64;       // weight rows per block (4 MFMA tiles of 16)
+constexpr int MX_TOK = 16;        // tokens per MFMA tile (v_mfma_f32_16x16x32_bf16 B side)
 
-template <bool GLU, int KSPLIT>
+// Scale-table row stride in 4-byte words for nc K chunks split over the waves: one word (four
+// E8M0 bytes) per chunk, rounded up to an odd count so the 16 rows of a tile hit distinct banks.
+__host__ __device__ inline int mx_scale_words(int nc) {
+  return ((nc + MX_WAVES - 1) / MX_WAVES) | 1;
+}
+
+// One block per (expert, 64 weight rows): gate/up rows ch..ch+31 of the gate and the same
+// channels of up (GLU), or 64 rows of the down projection. Wave w streams K chunks
+// [w*nc/4, (w+1)*nc/4) of all 64 rows; the partial sums meet in LDS.
+//
+// MFMA layout (16x16x32): lane l holds row l%16 of a 16-row weight tile and token l%16 of the
+// token tile; q = l/16 selects K. Within a 128-byte chunk lane q owns the weight bytes
+// [16q, 16q+16) and [64+16q, 64+16q+16), consumed as four K steps of 8 (the token fragments use
+// the same K order). A weight load instruction therefore covers 64 contiguous bytes of each of
+// 16 rows. Each such 16-byte run lies inside one 32-value scale block (q/2, then 2 + q/2).
+template <bool GLU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
-  constexpr int TPB = 4 / KSPLIT;  // row tiles per block
-  const int nb = (a.n_rtiles + TPB - 1) / TPB;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int nb = a.n_rtiles;
   const int e = (int)blockIdx.x / nb;
+  const int rt = (int)blockIdx.x % nb;
   const int m_begin = a.offsets[e], m_end = a.offsets[e + 1];
   if (m_begin >= m_end) return;
-  extern __shared__ __attribute__((aligned(16))) char xlds[];  // token rows, then partial sums
-  f32x16 (*red)[2][64] = (f32x16 (*)[2][64])xlds;
 
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int w = wv % KSPLIT;                                      // K part of this wave
-  const int rt = ((int)blockIdx.x % nb) * TPB + wv / KSPLIT;      // row tile of this wave
-  const bool tile_ok = rt < a.n_rtiles;
-  const int r = lane & 31, h = lane >> 5;
-  int row0, row1;
-  bool ok0, ok1;
-  if (GLU) {
-    const int ch = rt * 32 + r;
-    ok0 = ok1 = ch < a.I;
-    row0 = ok0 ? ch : 0;
-    row1 = ok1 ? a.I + ch : 0;
-  } else {
-    row0 = rt * 64 + r;
-    row1 = rt * 64 + 32 + r;
-    ok0 = row0 < a.R;
-    ok1 = row1 < a.R;
-    row0 = ok0 ? row0 : 0;
-    row1 = ok1 ? row1 : 0;
-  }
-  const uint8_t* w0 = a.W + (size_t)e * a.w_e + (size_t)row0 * a.w_ld;
-  const uint8_t* w1 = a.W + (size_t)e * a.w_e + (size_t)row1 * a.w_ld;
-  const uint8_t* s0 = a.S + (size_t)e * a.s_e + (size_t)row0 * a.s_ld;
-  const uint8_t* s1 = a.S + (size_t)e * a.s_e + (size_t)row1 * a.s_ld;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int rr = lane & 15, q = lane >> 4;
   const int nc = a.K / 128;
-  const int c_begin = w * nc / KSPLIT, c_end = tile_ok ? (w + 1) * nc / KSPLIT : c_begin;
+  const int c_begin = w * nc / MX_WAVES, c_end = (w + 1) * nc / MX_WAVES;
+  const int sw = mx_scale_words(nc);
+  uint32_t* stab = (uint32_t*)lds + w * MX_ROWS * sw;  // this wave's [64 rows][sw words]
+  char* xlds = lds + MX_WAVES * MX_ROWS * sw * 4;
+  const int x_bytes = MX_LDS - MX_WAVES * MX_ROWS * sw * 4;
 
-  for (int mb = m_begin; mb < m_end; mb += 32) {
-    const int m = mb + r;
-    const bool tok = m < m_end;
-    // Lanes past the group's last token read the first token's row: they only feed output
-    // columns that are never stored, and unconditional loads keep the pipeline's waits partial.
-    const int mm = tok ? m : m_begin;
-    const int xr = a.x_gather ? a.x_gather[mm] : mm;
-    const bf16* xrow = a.X + (size_t)xr * a.x_ld;
-    f32x16 acc0, acc1;
+  // Weight row of tile t for this lane (clamped to row 0 outside the matrix).
+  auto wrow = [&](int t, bool& ok) {
+    int row;
+    if (GLU) {
+      const int ch = rt * 32 + 16 * (t & 1) + rr;
+      ok = ch < a.I;
+      row = (t < 2 ? 0 : a.I) + ch;
+    } else {
+      row = rt * MX_ROWS + 16 * t + rr;
+      ok = row < a.R;
+    }
+    return ok ? row : 0;
+  };
+  const uint8_t* wp[4];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) { acc0[v] = 0.f; acc1[v] = 0.f; }
+  for (int t = 0; t < 4; ++t) {
+    bool ok;
+    wp[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(t, ok) * a.w_ld + 16 * q;
+  }
+  // Scale table: row i (tile i/16, lane row i%16) of this block, this wave's chunks.
+  {
+    const int nw = c_end - c_begin;
+    for (int u = lane; u < MX_ROWS * nw; u += 64) {
+      const int i = u / nw, c = u % nw;
+      int row;
+      if (GLU) {
+        const int ch = min(rt * 32 + 16 * ((i >> 4) & 1) + (i & 15), a.I - 1);
+        row = ((i >> 4) < 2 ? 0 : a.I) + ch;
+      } else {
+        row = min(rt * MX_ROWS + i, a.R - 1);
+      }
+      const uint8_t* sr = a.S + (size_t)e * a.s_e + (size_t)row * a.s_ld + (c_begin + c) * 4;
+      stab[i * sw + c] = *(const uint32_t*)sr;
+    }
+  }
 
-    // When this block's tokens fit in LDS (a decode batch gives an expert a handful), they are
-    // staged once and every wave reads its token fragments from LDS instead of re-reading 8 KB
-    // from L2 per 128-byte weight chunk; padding lanes read the last real token's row.
-    const int nt = min(32, m_end - mb);
-    const bool x_lds = (size_t)nt * a.K * sizeof(bf16) <= MX_XLDS;
+  for (int mb = m_begin; mb < m_end; mb += MX_TOK) {
+    const int nt = min(MX_TOK, m_end - mb);
+    const int m = mb + rr;
+    // Token rows: staged in LDS when they fit (a decode batch gives an expert a handful), else
+    // read from L2 per chunk. Lanes past the last token read the last token's row: they only
+    // feed output columns that are never stored.
+    const bool x_lds = (size_t)nt * a.K * sizeof(bf16) <= (size_t)x_bytes;
+    __syncthreads();  // scale table written; previous block's partial sums consumed
     if (x_lds) {
       const int units = a.K / 8;  // 16-byte units per token row
       for (int u = threadIdx.x; u < nt * units; u += blockDim.x) {
@@ -118,57 +142,52 @@ mx_gemm_kernel(MxArgs a) {
       }
       __syncthreads();
     }
-    const char* xl = xlds + (size_t)min(r, nt - 1) * a.K * sizeof(bf16);
+    const int mt = mb + min(rr, nt - 1);
+    const int xr = a.x_gather ? a.x_gather[mt] : mt;
+    const bf16* xrow = a.X + (size_t)xr * a.x_ld;
+    const char* xl = xlds + (size_t)min(rr, nt - 1) * a.K * sizeof(bf16);
 
-    // Software pipeline over two register buffers (no copies): everything chunk c+1 needs (token
-    // fragments, weights, scales) is issued before chunk c computes. Vector loads retire in issue
-    // order, so chunk c waits only for loads issued an iteration earlier. The prefetch is
-    // unconditional (the last one re-reads a valid chunk) so every path has the same count of
-    // loads in flight and the compiler's waits stay partial.
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Two register buffers of weight bytes (no copies): chunk c+1 is in flight while chunk c
+    // computes; the prefetch is unconditional (the last one re-reads a valid chunk) so every path
+    // has the same loads in flight and the compiler's waits stay partial.
     auto kloop = [&](auto xl_c) {
       constexpr bool XL = decltype(xl_c)::value;
-      struct Buf {
-        i32x4 x[XL ? 1 : 8];
-        uint4 a[4], b[4];
-        unsigned short sa, sb;
-      };
+      struct Buf { uint4 v[4][2]; };
       Buf p0, p1;
       auto fetch = [&](int c, Buf& f) {
-        const int kb = c * 128 + h * 64;
-        if constexpr (!XL) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) f.x[j] = ldg16(xrow + kb + 8 * j);
-        }
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f.a[i] = *(const uint4*)(w0 + kb + 16 * i);
-          f.b[i] = *(const uint4*)(w1 + kb + 16 * i);
-        }
-        f.sa = *(const unsigned short*)(s0 + kb / 32);
-        f.sb = *(const unsigned short*)(s1 + kb / 32);
-        __builtin_amdgcn_sched_barrier(0);  // issue the whole batch before the compute that follows
+          for (int t = 0; t < 4; ++t) f.v[t][j] = *(const uint4*)(wp[t] + c * 128 + 64 * j);
+        __builtin_amdgcn_sched_barrier(0);
       };
       auto compute = [&](const Buf& f, int c) {
-        i32x4 xv[8];
-        if constexpr (XL) {
-          const int kb = c * 128 + h * 64;
+        // token fragments of the four K steps
+        i32x4 xv[4];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xv[j] = *(const i32x4*)(xl + (kb + 8 * j) * sizeof(bf16));
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) xv[j] = f.x[j];
+        for (int ks = 0; ks < 4; ++ks) {
+          const int k = c * 128 + (ks >> 1) * 64 + 16 * q + 8 * (ks & 1);
+          if constexpr (XL) xv[ks] = *(const i32x4*)(xl + k * sizeof(bf16));
+          else xv[ks] = ldg16(xrow + k);
         }
-        const float sa0 = e8m0_to_f32(f.sa & 0xff), sa1 = e8m0_to_f32(f.sa >> 8);
-        const float sb0 = e8m0_to_f32(f.sb & 0xff), sb1 = e8m0_to_f32(f.sb >> 8);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint4 ua = f.a[j >> 1], ub = f.b[j >> 1];
-          const i32x4 av = (j & 1) ? dequant8(ua.z, ua.w, j < 4 ? sa0 : sa1)
-                                   : dequant8(ua.x, ua.y, j < 4 ? sa0 : sa1);
-          const i32x4 bv = (j & 1) ? dequant8(ub.z, ub.w, j < 4 ? sb0 : sb1)
-                                   : dequant8(ub.x, ub.y, j < 4 ? sb0 : sb1);
-          Mfma<bf16>::step(acc0, av, xv[j]);
-          Mfma<bf16>::step(acc1, bv, xv[j]);
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t sc = stab[(16 * t + rr) * sw + (c - c_begin)];
+          const float s0 = e8m0_to_f32((sc >> (8 * (q >> 1))) & 0xff);
+          const float s1 = e8m0_to_f32((sc >> (8 * (2 + (q >> 1)))) & 0xff);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const uint4 u = f.v[t][ks >> 1];
+            const i32x4 av = (ks & 1) ? dequant8(u.z, u.w, (ks >> 1) ? s1 : s0)
+                                      : dequant8(u.x, u.y, (ks >> 1) ? s1 : s0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                             __builtin_bit_cast(bf16x8, xv[ks]),
+                                                             acc[t], 0, 0, 0);
+          }
         }
       };
       const int c_last = c_end - 1;
@@ -185,55 +204,47 @@ mx_gemm_kernel(MxArgs a) {
     };
     if (x_lds) kloop(std::true_type{});
     else kloop(std::false_type{});
-    // The partial-sum exchange below reuses the LDS that held the tokens.
-    if (KSPLIT > 1 && x_lds) __syncthreads();
 
-    if (KSPLIT > 1) {
-      if (w > 0) {
-        red[wv][0][lane] = acc0;
-        red[wv][1][lane] = acc1;
-      }
-      __syncthreads();
-      if (w == 0) {
+    // Partial sums of waves 1-3 meet wave 0's in LDS (reusing the token rows' space).
+    f32x4* red = (f32x4*)xlds;  // [wave][tile][lane]
+    __syncthreads();
+    if (w > 0) {
 #pragma unroll
-        for (int q = 1; q < KSPLIT; ++q) {
-          const f32x16 p0 = red[wv + q][0][lane], p1 = red[wv + q][1][lane];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) { acc0[v] += p0[v]; acc1[v] += p1[v]; }
-        }
-      }
+      for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
     }
-    if (w == 0 && tok && tile_ok) {
-      bf16* o = a.out + (size_t)m * a.out_ld;
+    __syncthreads();
+    if (w == 0) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i0 = 8 * g + 4 * h;  // row within the 32-row tile
+      for (int v = 1; v < MX_WAVES; ++v)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const f32x4 p = red[(v * 4 + t) * 64 + lane];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[t][j] += p[j];
+        }
+      // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
+      if (rr < nt) {
+        bf16* o = a.out + (size_t)m * a.out_ld;
         if (GLU) {
-          if (rt * 32 + i0 < a.I) {
-            float iv[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) iv[j] = silu(acc0[4 * g + j]) * acc1[4 * g + j];
-            const bf16x2 p = {(bf16)iv[0], (bf16)iv[1]}, q = {(bf16)iv[2], (bf16)iv[3]};
-            *(uint2*)(o + rt * 32 + i0) =
-                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
+          for (int t = 0; t < 2; ++t) {
+            const int ch = rt * 32 + 16 * t + 4 * q;
+            if (ch < a.I) {
+              float iv[4];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) iv[j] = silu(acc[t][j]) * acc[t + 2][j];
+              Store4<bf16>::st(o + ch, iv[0], iv[1], iv[2], iv[3]);
+            }
           }
         } else {
-          if (rt * 64 + i0 < a.R) {
-            const bf16x2 p = {(bf16)acc0[4 * g], (bf16)acc0[4 * g + 1]};
-            const bf16x2 q = {(bf16)acc0[4 * g + 2], (bf16)acc0[4 * g + 3]};
-            *(uint2*)(o + rt * 64 + i0) =
-                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
-          }
-          if (rt * 64 + 32 + i0 < a.R) {
-            const bf16x2 p = {(bf16)acc1[4 * g], (bf16)acc1[4 * g + 1]};
-            const bf16x2 q = {(bf16)acc1[4 * g + 2], (bf16)acc1[4 * g + 3]};
-            *(uint2*)(o + rt * 64 + 32 + i0) =
-                uint2{__builtin_bit_cast(unsigned, p), __builtin_bit_cast(unsigned, q)};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int row = rt * MX_ROWS + 16 * t + 4 * q;
+            if (row < a.R) Store4<bf16>::st(o + row, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
           }
         }
       }
     }
-    if (KSPLIT > 1) __syncthreads();
   }
 }
 
@@ -243,19 +254,12 @@ using namespace moe;
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// ksplit = waves per row tile (4: each block is one row tile with K split four ways; measured
-// within a few percent of 2 and 1 for both kernels at the decode shape).
 template <bool GLU>
-static bool launch_mx(const MxArgs& a, int E, int ksplit, hipStream_t s) {
-  const int tpb = 4 / ksplit;
-  const unsigned grid = (unsigned)(E * ((a.n_rtiles + tpb - 1) / tpb));
-  auto go = [&](auto kern) {
-    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)MX_XLDS);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), MX_XLDS, s, a);
-  };
-  if (ksplit == 1) go(mx_gemm_kernel<GLU, 1>);
-  else if (ksplit == 2) go(mx_gemm_kernel<GLU, 2>);
-  else go(mx_gemm_kernel<GLU, 4>);
+static bool launch_mx(const MxArgs& a, int E, hipStream_t s) {
+  const unsigned grid = (unsigned)(E * a.n_rtiles);
+  auto kern = mx_gemm_kernel<GLU>;
+  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MX_LDS);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * MX_WAVES), MX_LDS, s, a);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -271,8 +275,12 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
       !inter || !eo)
     return MOE_ERR_SHAPE;
   if (!al16(hidden) || !al16(w13_q) || !al16(w2_q) || !al16(inter) || !al16(eo) ||
-      ((uintptr_t)w13_scale & 1) || ((uintptr_t)w2_scale & 1))
+      ((uintptr_t)w13_scale & 3) || ((uintptr_t)w2_scale & 3))
     return MOE_ERR_ALIGN;
+  // The scale tables of a block plus the partial sums (16 KB) must fit the block's LDS.
+  for (int64_t k : {H, I})
+    if ((int64_t)mx_scale_words((int)(k / 128)) * 4 * MX_ROWS * MX_WAVES + 16384 > MX_LDS)
+      return MOE_ERR_SHAPE;
   if ((int64_t)E * ((2 * I + 63) / 64) >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   MxArgs g = {};
@@ -280,15 +288,15 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
   g.S = (const uint8_t*)w13_scale; g.s_e = 2 * I * (H / 32); g.s_ld = H / 32;
   g.R = (int)(2 * I); g.K = (int)H; g.I = (int)I;
   g.X = (const bf16*)hidden; g.x_ld = H; g.x_gather = sorted_token;
-  g.offsets = offsets; g.n_rtiles = (int)((I + 31) / 32);
+  g.offsets = offsets; g.n_rtiles = (int)((I + 31) / 32);  // 32 channels: 32 gate + 32 up rows
   g.out = (bf16*)inter; g.out_ld = I;
-  if (!launch_mx<true>(g, E, 4, s)) return MOE_ERR_LAUNCH;
+  if (!launch_mx<true>(g, E, s)) return MOE_ERR_LAUNCH;
   MxArgs d = {};
   d.W = (const uint8_t*)w2_q; d.w_e = H * I; d.w_ld = I;
   d.S = (const uint8_t*)w2_scale; d.s_e = H * (I / 32); d.s_ld = I / 32;
   d.R = (int)H; d.K = (int)I; d.I = (int)I;
   d.X = (const bf16*)inter; d.x_ld = I; d.x_gather = nullptr;
-  d.offsets = offsets; d.n_rtiles = (int)((H + 63) / 64);
+  d.offsets = offsets; d.n_rtiles = (int)((H + MX_ROWS - 1) / MX_ROWS);
   d.out = (bf16*)eo; d.out_ld = H;
-  return launch_mx<false>(d, E, 4, s) ? MOE_OK : MOE_ERR_LAUNCH;
+  return launch_mx<false>(d, E, s) ? MOE_OK : MOE_ERR_LAUNCH;
 }
