@@ -10,6 +10,7 @@
 //   pass 3 (scatter): each chunk re-reads its rows and ranks them stably. Within a wave the rank
 //                     of a row among equal experts comes from a ballot match (one ballot per id
 //                     bit) and a popcount; waves of one step are ordered through LDS counters.
+// A batch that fits one chunk runs all three passes in one workgroup (dispatch_small_kernel).
 #include "moe_common.h"
 
 namespace moe {
@@ -152,6 +153,101 @@ dispatch_scatter_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, i
   }
 }
 
+// All three passes in one workgroup when every row fits one chunk (decode-sized batches), with
+// block barriers in place of kernel launches: LDS histogram, the scans of dispatch_scan_kernel,
+// and the stable scatter of dispatch_scatter_kernel over steps of SMALL_THREADS rows.
+constexpr int SMALL_THREADS = 512;
+__global__ void __launch_bounds__(SMALL_THREADS)
+dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int E,
+                      int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                      int32_t* __restrict__ tile_offsets, int32_t* __restrict__ expert_order,
+                      int32_t* __restrict__ sorted_token, int32_t* __restrict__ sorted_flat,
+                      int32_t* __restrict__ flat_to_sorted, int32_t* __restrict__ status) {
+  constexpr int NW = SMALL_THREADS / 64;
+  __shared__ int cnt[MAX_EXPERTS + 1];
+  __shared__ int run[MAX_EXPERTS + 1];
+  __shared__ int wcnt[NW][MAX_EXPERTS + 1];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e <= E; e += SMALL_THREADS) cnt[e] = 0;
+  if (tid == 0) s_bad = 0;
+  __syncthreads();
+  int bad = 0;
+  for (int64_t f = tid; f < M; f += SMALL_THREADS) {
+    bool valid;
+    const int e = load_expert(idx, f, E, valid);
+    atomicAdd(&cnt[e], 1);
+    bad += valid ? 0 : 1;
+  }
+  if (bad) atomicAdd(&s_bad, bad);
+  __syncthreads();
+  if (tid == 0) {
+    int o = 0, tt = 0;
+    for (int i = 0; i < E; ++i) {
+      offsets[i] = o;
+      tile_offsets[i] = tt;
+      run[i] = o;
+      o += cnt[i];
+      tt += (cnt[i] + TILE_ROWS - 1) / TILE_ROWS;
+    }
+    offsets[E] = o;
+    tile_offsets[E] = tt;
+    if (s_bad) atomicAdd(status, s_bad);
+  }
+  // Experts by descending count (ties by id).
+  for (int e = tid; e < E; e += SMALL_THREADS) {
+    const int c = cnt[e];
+    counts[e] = c;
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+      const int cj = cnt[j];
+      rank += (cj > c) || (cj == c && j < e);
+    }
+    expert_order[rank] = e;
+  }
+  int nbits = 0;
+  while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E = invalid bucket)
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  for (int64_t s = 0; s < M; s += SMALL_THREADS) {
+    for (int i = tid; i < NW * (E + 1); i += SMALL_THREADS) wcnt[i / (E + 1)][i % (E + 1)] = 0;
+    __syncthreads();  // also orders run[] (first step) after thread 0's scan
+    const int64_t f = s + tid;
+    const bool live = f < M;
+    bool valid = false;
+    const int e = live ? load_expert(idx, f, E, valid) : E;
+    unsigned long long match = ballot64(live);
+#pragma unroll 1
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (e >> bit) & 1;
+      const unsigned long long bl = ballot64(live && on);
+      match &= on ? bl : ~bl;
+    }
+    if (!live) match = 0;
+    const int rank = __popcll(match & lt_mask);
+    if (live && rank == 0) wcnt[w][e] = __popcll(match);
+    __syncthreads();
+    if (live) {
+      if (valid) {
+        int pos = run[e] + rank;
+        for (int ww = 0; ww < w; ++ww) pos += wcnt[ww][e];
+        sorted_token[pos] = (int32_t)(f / top_k);
+        sorted_flat[pos] = (int32_t)f;
+        flat_to_sorted[f] = pos;
+      } else {
+        flat_to_sorted[f] = -1;
+      }
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += SMALL_THREADS) {
+      int add = 0;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) add += wcnt[ww][ee];
+      run[ee] += add;
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -185,6 +281,12 @@ extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int 
   hipStream_t s = (hipStream_t)stream;
   int32_t* hist = (int32_t*)workspace;
   const int nc = (int)n_chunks(M);
+  if (nc <= 1) {
+    hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(SMALL_THREADS), 0, s, top_k_indices, M,
+                       top_k, n_experts, counts, offsets, tile_offsets, expert_order, sorted_token,
+                       sorted_flat, flat_to_sorted, status);
+    return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+  }
   if (nc > 0) {
     hipLaunchKernelGGL(dispatch_hist_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s, top_k_indices,
                        M, n_experts, hist, status);
