@@ -59,22 +59,35 @@ __host__ __device__ inline int mx_scale_words(int nc) {
   return ((nc + MX_WAVES - 1) / MX_WAVES) | 1;
 }
 
-// One block per (expert, 64 weight rows): gate/up rows ch..ch+31 of the gate and the same
-// channels of up (GLU), or 64 rows of the down projection. Wave w streams K chunks
-// [w*nc/4, (w+1)*nc/4) of all 64 rows; the partial sums meet in LDS.
+// One block per (expert, RT consecutive row tiles of 64 weight rows): gate/up tile = rows
+// ch..ch+31 of the gate and the same channels of up (GLU), down tile = 64 rows. The block stages
+// the expert's token rows once and runs its row tiles one after the other over them. Wave w
+// streams K chunks [w*nc/4, (w+1)*nc/4) of all 64 rows of a tile; the partial sums meet in LDS.
 //
 // MFMA layout (16x16x32): lane l holds row l%16 of a 16-row weight tile and token l%16 of the
 // token tile; q = l/16 selects K. Within a 128-byte chunk lane q owns the weight bytes
 // [16q, 16q+16) and [64+16q, 64+16q+16), consumed as four K steps of 8 (the token fragments use
 // the same K order). A weight load instruction therefore covers 64 contiguous bytes of each of
 // 16 rows. Each such 16-byte run lies inside one 32-value scale block (q/2, then 2 + q/2).
-template <bool GLU>
+//
+// LDS: RT x 4 per-wave scale tables ([64 rows][sw words] each), then (RT > 1) the partial-sum
+// exchange, then the staged token rows (RT == 1: the exchange reuses the token rows' space).
+constexpr int MX_RED_BYTES = MX_WAVES * 4 * 64 * 16;  // [wave][tile][lane] f32x4
+__host__ __device__ inline int mx_table_bytes(int nc, int rt) {
+  return rt * MX_WAVES * MX_ROWS * mx_scale_words(nc) * 4;
+}
+__host__ __device__ inline int mx_x_offset(int nc, int rt) {
+  return mx_table_bytes(nc, rt) + (rt > 1 ? MX_RED_BYTES : 0);
+}
+
+template <bool GLU, int RT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  const int nb = a.n_rtiles;
-  const int e = (int)blockIdx.x / nb;
-  const int rt = (int)blockIdx.x % nb;
+  const int ng = (a.n_rtiles + RT - 1) / RT;
+  const int e = (int)blockIdx.x / ng;
+  const int rt0 = ((int)blockIdx.x % ng) * RT;
+  const int nrt = min(RT, a.n_rtiles - rt0);
   const int m_begin = a.offsets[e], m_end = a.offsets[e + 1];
   if (m_begin >= m_end) return;
 
@@ -83,43 +96,29 @@ mx_gemm_kernel(MxArgs a) {
   const int nc = a.K / 128;
   const int c_begin = w * nc / MX_WAVES, c_end = (w + 1) * nc / MX_WAVES;
   const int sw = mx_scale_words(nc);
-  uint32_t* stab = (uint32_t*)lds + w * MX_ROWS * sw;  // this wave's [64 rows][sw words]
-  char* xlds = lds + MX_WAVES * MX_ROWS * sw * 4;
-  const int x_bytes = MX_LDS - MX_WAVES * MX_ROWS * sw * 4;
+  auto stab_of = [&](int j) { return (uint32_t*)lds + (j * MX_WAVES + w) * MX_ROWS * sw; };
+  char* xlds = lds + mx_x_offset(nc, RT);
+  f32x4* red = (f32x4*)(RT > 1 ? lds + mx_table_bytes(nc, RT) : xlds);
+  const int x_bytes = MX_LDS - mx_x_offset(nc, RT);
 
-  // Weight row of tile t for this lane (clamped to row 0 outside the matrix).
-  auto wrow = [&](int t, bool& ok) {
-    int row;
+  // Weight row i of tile rt (clamped into the matrix; rows outside it feed unstored outputs).
+  auto wrow = [&](int rt, int i) {
     if (GLU) {
-      const int ch = rt * 32 + 16 * (t & 1) + rr;
-      ok = ch < a.I;
-      row = (t < 2 ? 0 : a.I) + ch;
-    } else {
-      row = rt * MX_ROWS + 16 * t + rr;
-      ok = row < a.R;
+      const int ch = min(rt * 32 + 16 * ((i >> 4) & 1) + (i & 15), a.I - 1);
+      return ((i >> 4) < 2 ? 0 : a.I) + ch;
     }
-    return ok ? row : 0;
+    return min(rt * MX_ROWS + i, a.R - 1);
   };
-  const uint8_t* wp[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    bool ok;
-    wp[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(t, ok) * a.w_ld + 16 * q;
-  }
-  // Scale table: row i (tile i/16, lane row i%16) of this block, this wave's chunks.
+  // Scale tables: row i of tile j, this wave's chunks.
   {
     const int nw = c_end - c_begin;
-    for (int u = lane; u < MX_ROWS * nw; u += 64) {
-      const int i = u / nw, c = u % nw;
-      int row;
-      if (GLU) {
-        const int ch = min(rt * 32 + 16 * ((i >> 4) & 1) + (i & 15), a.I - 1);
-        row = ((i >> 4) < 2 ? 0 : a.I) + ch;
-      } else {
-        row = min(rt * MX_ROWS + i, a.R - 1);
+    for (int j = 0; j < nrt; ++j) {
+      uint32_t* stab = stab_of(j);
+      for (int u = lane; u < MX_ROWS * nw; u += 64) {
+        const int i = u / nw, c = u % nw;
+        const uint8_t* sr = a.S + (size_t)e * a.s_e + (size_t)wrow(rt0 + j, i) * a.s_ld + (c_begin + c) * 4;
+        stab[i * sw + c] = *(const uint32_t*)sr;
       }
-      const uint8_t* sr = a.S + (size_t)e * a.s_e + (size_t)row * a.s_ld + (c_begin + c) * 4;
-      stab[i * sw + c] = *(const uint32_t*)sr;
     }
   }
 
@@ -130,7 +129,7 @@ mx_gemm_kernel(MxArgs a) {
     // read from L2 per chunk. Lanes past the last token read the last token's row: they only
     // feed output columns that are never stored.
     const bool x_lds = (size_t)nt * a.K * sizeof(bf16) <= (size_t)x_bytes;
-    __syncthreads();  // scale table written; previous block's partial sums consumed
+    __syncthreads();  // scale tables written; the previous token block is done with the LDS
     if (x_lds) {
       const int units = a.K / 8;  // 16-byte units per token row
       for (int u = threadIdx.x; u < nt * units; u += blockDim.x) {
@@ -147,103 +146,110 @@ mx_gemm_kernel(MxArgs a) {
     const bf16* xrow = a.X + (size_t)xr * a.x_ld;
     const char* xl = xlds + (size_t)min(rr, nt - 1) * a.K * sizeof(bf16);
 
-    f32x4 acc[4];
+    for (int j = 0; j < nrt; ++j) {
+      const int rt = rt0 + j;
+      const uint32_t* stab = stab_of(j);
+      const uint8_t* wp[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < 4; ++t)
+        wp[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt, 16 * t + rr) * a.w_ld + 16 * q;
+      f32x4 acc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Two register buffers of weight bytes (no copies): chunk c+1 is in flight while chunk c
-    // computes; the prefetch is unconditional (the last one re-reads a valid chunk) so every path
-    // has the same loads in flight and the compiler's waits stay partial.
-    auto kloop = [&](auto xl_c) {
-      constexpr bool XL = decltype(xl_c)::value;
-      struct Buf { uint4 v[4][2]; };
-      Buf p0, p1;
-      auto fetch = [&](int c, Buf& f) {
+      // Two register buffers of weight bytes (no copies): chunk c+1 is in flight while chunk c
+      // computes; the prefetch is unconditional (the last one re-reads a valid chunk) so every
+      // path has the same loads in flight and the compiler's waits stay partial.
+      auto kloop = [&](auto xl_c) {
+        constexpr bool XL = decltype(xl_c)::value;
+        struct Buf { uint4 v[4][2]; };
+        Buf p0, p1;
+        auto fetch = [&](int c, Buf& f) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+          for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) f.v[t][j] = *(const uint4*)(wp[t] + c * 128 + 64 * j);
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      auto compute = [&](const Buf& f, int c) {
-        // token fragments of the four K steps
-        i32x4 xv[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const int k = c * 128 + (ks >> 1) * 64 + 16 * q + 8 * (ks & 1);
-          if constexpr (XL) xv[ks] = *(const i32x4*)(xl + k * sizeof(bf16));
-          else xv[ks] = ldg16(xrow + k);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const uint32_t sc = stab[(16 * t + rr) * sw + (c - c_begin)];
-          const float s0 = e8m0_to_f32((sc >> (8 * (q >> 1))) & 0xff);
-          const float s1 = e8m0_to_f32((sc >> (8 * (2 + (q >> 1)))) & 0xff);
+            for (int t = 0; t < 4; ++t) f.v[t][jj] = *(const uint4*)(wp[t] + c * 128 + 64 * jj);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        auto compute = [&](const Buf& f, int c) {
+          i32x4 xv[4];  // token fragments of the four K steps
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
-            const uint4 u = f.v[t][ks >> 1];
-            const i32x4 av = (ks & 1) ? dequant8(u.z, u.w, (ks >> 1) ? s1 : s0)
-                                      : dequant8(u.x, u.y, (ks >> 1) ? s1 : s0);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
-                                                             __builtin_bit_cast(bf16x8, xv[ks]),
-                                                             acc[t], 0, 0, 0);
+            const int k = c * 128 + (ks >> 1) * 64 + 16 * q + 8 * (ks & 1);
+            if constexpr (XL) xv[ks] = *(const i32x4*)(xl + k * sizeof(bf16));
+            else xv[ks] = ldg16(xrow + k);
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t sc = stab[(16 * t + rr) * sw + (c - c_begin)];
+            const float s0 = e8m0_to_f32((sc >> (8 * (q >> 1))) & 0xff);
+            const float s1 = e8m0_to_f32((sc >> (8 * (2 + (q >> 1)))) & 0xff);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+              const uint4 u = f.v[t][ks >> 1];
+              const i32x4 av = (ks & 1) ? dequant8(u.z, u.w, (ks >> 1) ? s1 : s0)
+                                        : dequant8(u.x, u.y, (ks >> 1) ? s1 : s0);
+              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                               __builtin_bit_cast(bf16x8, xv[ks]),
+                                                               acc[t], 0, 0, 0);
+            }
+          }
+        };
+        const int c_last = c_end - 1;
+        if (c_begin <= c_last) {
+          fetch(c_begin, p0);
+          for (int c = c_begin; c <= c_last; c += 2) {
+            fetch(min(c + 1, c_last), p1);
+            compute(p0, c);
+            if (c + 1 > c_last) break;
+            fetch(min(c + 2, c_last), p0);
+            compute(p1, c + 1);
           }
         }
       };
-      const int c_last = c_end - 1;
-      if (c_begin <= c_last) {
-        fetch(c_begin, p0);
-        for (int c = c_begin; c <= c_last; c += 2) {
-          fetch(min(c + 1, c_last), p1);
-          compute(p0, c);
-          if (c + 1 > c_last) break;
-          fetch(min(c + 2, c_last), p0);
-          compute(p1, c + 1);
-        }
-      }
-    };
-    if (x_lds) kloop(std::true_type{});
-    else kloop(std::false_type{});
+      if (x_lds) kloop(std::true_type{});
+      else kloop(std::false_type{});
 
-    // Partial sums of waves 1-3 meet wave 0's in LDS (reusing the token rows' space).
-    f32x4* red = (f32x4*)xlds;  // [wave][tile][lane]
-    __syncthreads();
-    if (w > 0) {
+      // Partial sums of waves 1-3 meet wave 0's in LDS.
+      if (RT == 1) __syncthreads();  // the exchange reuses the token rows' space
+      if (w > 0) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
-    }
-    __syncthreads();
-    if (w == 0) {
+        for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
+      }
+      __syncthreads();
+      if (w == 0) {
 #pragma unroll
-      for (int v = 1; v < MX_WAVES; ++v)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f32x4 p = red[(v * 4 + t) * 64 + lane];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[t][j] += p[j];
-        }
-      // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
-      if (rr < nt) {
-        bf16* o = a.out + (size_t)m * a.out_ld;
-        if (GLU) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const int ch = rt * 32 + 16 * t + 4 * q;
-            if (ch < a.I) {
-              float iv[4];
-#pragma unroll
-              for (int j = 0; j < 4; ++j) iv[j] = silu(acc[t][j]) * acc[t + 2][j];
-              Store4<bf16>::st(o + ch, iv[0], iv[1], iv[2], iv[3]);
-            }
-          }
-        } else {
+        for (int v = 1; v < MX_WAVES; ++v)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const int row = rt * MX_ROWS + 16 * t + 4 * q;
-            if (row < a.R) Store4<bf16>::st(o + row, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            const f32x4 p = red[(v * 4 + t) * 64 + lane];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) acc[t][jj] += p[jj];
+          }
+        // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
+        if (rr < nt) {
+          bf16* o = a.out + (size_t)m * a.out_ld;
+          if (GLU) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const int ch = rt * 32 + 16 * t + 4 * q;
+              if (ch < a.I) {
+                float iv[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) iv[jj] = silu(acc[t][jj]) * acc[t + 2][jj];
+                Store4<bf16>::st(o + ch, iv[0], iv[1], iv[2], iv[3]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int row = rt * MX_ROWS + 16 * t + 4 * q;
+              if (row < a.R) Store4<bf16>::st(o + row, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            }
           }
         }
       }
+      if (RT > 1) __syncthreads();  // wave 0 has read the exchange before the next tile writes it
     }
   }
 }
@@ -254,12 +260,25 @@ using namespace moe;
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Row tiles per block: several when the scale tables of that many tiles, the partial-sum
+// exchange and at least 16 KB of token rows fit the block's LDS.
+#ifndef MX_RT_GLU
+#define MX_RT_GLU 2
+#endif
+#ifndef MX_RT_DOWN
+#define MX_RT_DOWN 2
+#endif
 template <bool GLU>
 static bool launch_mx(const MxArgs& a, int E, hipStream_t s) {
-  const unsigned grid = (unsigned)(E * a.n_rtiles);
-  auto kern = mx_gemm_kernel<GLU>;
-  (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MX_LDS);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * MX_WAVES), MX_LDS, s, a);
+  constexpr int MX_RT = GLU ? MX_RT_GLU : MX_RT_DOWN;
+  const int nc = a.K / 128;
+  auto go = [&](auto kern, int rt) {
+    const unsigned grid = (unsigned)(E * ((a.n_rtiles + rt - 1) / rt));
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MX_LDS);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * MX_WAVES), MX_LDS, s, a);
+  };
+  if (MX_RT > 1 && mx_x_offset(nc, MX_RT) + 16384 <= MX_LDS) go(mx_gemm_kernel<GLU, MX_RT>, MX_RT);
+  else go(mx_gemm_kernel<GLU, 1>, 1);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -279,7 +298,7 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
     return MOE_ERR_ALIGN;
   // The scale tables of a block plus the partial sums (16 KB) must fit the block's LDS.
   for (int64_t k : {H, I})
-    if ((int64_t)mx_scale_words((int)(k / 128)) * 4 * MX_ROWS * MX_WAVES + 16384 > MX_LDS)
+    if (mx_x_offset((int)(k / 128), 1) + MX_RED_BYTES > MX_LDS)
       return MOE_ERR_SHAPE;
   if ((int64_t)E * ((2 * I + 63) / 64) >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
