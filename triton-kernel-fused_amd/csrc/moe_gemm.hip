@@ -610,17 +610,29 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
 // of rsrc[rrow(m), r] * csrc[crow(m), c]; both operands row-contiguous (optionally gathered rows).
 template <typename T, bool RG, bool CG>
 __global__ void __launch_bounds__(v4::NT, 1)
-wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical) {
+wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int xr, int xc) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  // Round-robin over the XCDs (no regrouping): `order` puts the largest experts first, and each of
-  // them is spread over all 8 XCDs; tiles that land on one XCD share their r-slice (rt fastest).
+  // `order` puts the largest experts first and each expert's tiles are spread over all 8 XCDs
+  // (workgroups are dealt to XCDs round-robin, so tile j of an expert runs on XCD j % 8 when the
+  // tile count is a multiple of 8). With xr > 0 the r x c tile grid is cut into 8 rectangles of
+  // xr x xc tiles and XCD x takes rectangle x, so the tiles sharing one L2 read xr r-slices and
+  // xc c-slices; otherwise tiles sharing an XCD share their r-slice (rt fastest).
   const int lid = (int)blockIdx.x;
   if (lid >= n_logical) return;
   const int per_e = a.n_rtiles * a.n_ctiles;
   const int ei = lid / per_e, rem = lid % per_e;
   const int e = order ? order[ei] : ei;
   if (e < 0 || e >= E_glu) return;  // weightless special expert
-  const int ct = rem / a.n_rtiles, rt = rem % a.n_rtiles;
+  int ct, rt;
+  if (xr > 0) {
+    const int x = rem & 7, i = rem >> 3;              // XCD, index within its rectangle
+    const int nrx = a.n_rtiles / xr;                  // rectangles along r
+    rt = (x % nrx) * xr + i % xr;
+    ct = (x / nrx) * xc + i / xr;
+  } else {
+    ct = rem / a.n_rtiles;
+    rt = rem % a.n_rtiles;
+  }
   const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
   const int r0 = rt * v4::TILE, c0 = ct * v4::TILE;
   const int wr = v4::wave_r(), wc = v4::wave_c();
@@ -792,9 +804,22 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   auto kern = a.r_gather ? (a.c_gather ? wgrad_v4_kernel<T, true, true> : wgrad_v4_kernel<T, true, false>)
                          : (a.c_gather ? wgrad_v4_kernel<T, false, true> : wgrad_v4_kernel<T, false, false>);
+  // Per-XCD rectangles (see wgrad_v4_kernel): 8 equal rectangles of xr x xc tiles with the fewest
+  // slices per rectangle (xr + xc); 0 = the r-slice mapping (grids that do not split into 8).
+  int xr = 0, xc = 0;
+  for (int nrx : {1, 2, 4, 8}) {  // rectangles along r; 8 / nrx along c
+    const int ncx = 8 / nrx;
+    if (a.n_rtiles % nrx == 0 && a.n_ctiles % ncx == 0) {
+      const int r = a.n_rtiles / nrx, c = a.n_ctiles / ncx;
+      if (xr == 0 || r + c < xr + xc) {
+        xr = r;
+        xc = c;
+      }
+    }
+  }
   (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, order, E_glu,
-                     (int)logical);
+                     (int)logical, xr, xc);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
