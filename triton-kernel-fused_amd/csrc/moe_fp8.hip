@@ -88,49 +88,73 @@ fp8_gemm_kernel(Fp8Args a, int n_logical) {
   __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
   v4::mainloop_ring<fp8e4m3>(acc, lp, lq, 0, a.K, smem);
 
-  // Epilogue from registers: lane (l & 31) of fragment tj is token row m; each lane holds four
+  // Epilogue: scales applied in fp32 in registers, then the bf16 results of each wave are staged
+  // in its own LDS block (the ring's final barrier has released the LDS) and stored as whole row
+  // segments: lane (l & 31) of fragment tj is token row q = 32 tj + (l & 31) and holds four
   // consecutive output channels per 8-channel group g (half h of the lane).
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
+  const int w = threadIdx.x >> 6;
   const float* ps = a.p_scale + (size_t)e * a.ps_e;
-  static_for<0, v4::TJ>([&](auto tj_c) {
-    constexpr int tj = decltype(tj_c)::value;
+  float qsv[v4::TJ];
+#pragma unroll
+  for (int tj = 0; tj < v4::TJ; ++tj) {
     const int m = m0 + wc * v4::WQ + tj * 32 + (lane & 31);
-    if (m >= m_end) return;
-    const float qs = a.q_scale[a.q_gather ? a.q_gather[m] : m];
-    if constexpr (GLU) {
-      bf16* it = a.out + (size_t)m * a.I;
+    qsv[tj] = m < m_end ? a.q_scale[a.q_gather ? a.q_gather[m] : m] : 0.f;
+  }
+  const int row0 = m0 + wc * v4::WQ;
+  if constexpr (GLU) {
+    // inter block of the wave: 64 token rows x 64 channels (128 bytes), 16-byte chunk c of row
+    // q at c ^ (q & 7).
+    char* wl = smem + w * (v4::WQ * 128);
 #pragma unroll
-      for (int ti = 0; ti < v4::TI / 2; ++ti)
+    for (int ti = 0; ti < v4::TI / 2; ++ti)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + ti * 32 + 8 * g + 4 * h;
-          if (ch >= a.I) continue;
-          const f32x4 sg = *(const f32x4*)(ps + ch);
-          const f32x4 su = *(const f32x4*)(ps + a.I + ch);
+      for (int g = 0; g < 4; ++g) {
+        const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + ti * 32 + 8 * g + 4 * h;
+        const bool cok = ch < a.I;
+        const f32x4 sg = cok ? *(const f32x4*)(ps + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 su = cok ? *(const f32x4*)(ps + a.I + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tj = 0; tj < v4::TJ; ++tj) {
           float iv[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float gv = acc[ti][tj][4 * g + j] * qs * sg[j];
-            const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qs * su[j];
+            const float gv = acc[ti][tj][4 * g + j] * qsv[tj] * sg[j];
+            const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qsv[tj] * su[j];
             iv[j] = silu(gv) * uv;
           }
-          Store4<bf16>::st(it + ch, iv[0], iv[1], iv[2], iv[3]);
+          const int q = tj * 32 + (lane & 31);
+          const uint2 v = {v2::pack2<bf16>(iv[0], iv[1]), v2::pack2<bf16>(iv[2], iv[3])};
+          *(uint2*)(wl + q * 128 + (((4 * ti + g) ^ (q & 7)) << 4) + 8 * h) = v;
         }
-    } else {
-      bf16* o = a.out + (size_t)m * a.out_ld;
-#pragma unroll
-      for (int ti = 0; ti < v4::TI; ++ti)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int r = rt * v4::TILE + wr * v4::WP + ti * 32 + 8 * g + 4 * h;
-          if (r >= a.R) continue;
-          const f32x4 sr = *(const f32x4*)(ps + r);
-          Store4<bf16>::st(o + r, acc[ti][tj][4 * g] * qs * sr[0], acc[ti][tj][4 * g + 1] * qs * sr[1],
-                           acc[ti][tj][4 * g + 2] * qs * sr[2], acc[ti][tj][4 * g + 3] * qs * sr[3]);
-        }
+      }
+    __syncthreads();
+    const int c = lane & 7;
+    const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + 8 * c;
+#pragma unroll 4
+    for (int it = 0; it < v4::WQ / 8; ++it) {
+      const int q = it * 8 + (lane >> 3);
+      const i32x4 v = *(const i32x4*)(wl + q * 128 + ((c ^ (q & 7)) << 4));
+      if (row0 + q < m_end && ch < a.I) *(i32x4*)(a.out + (size_t)(row0 + q) * a.I + ch) = v;
     }
-  });
+  } else {
+#pragma unroll
+    for (int ti = 0; ti < v4::TI; ++ti)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r = rt * v4::TILE + wr * v4::WP + ti * 32 + 8 * g + 4 * h;
+        const f32x4 sr = r < a.R ? *(const f32x4*)(ps + r) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tj = 0; tj < v4::TJ; ++tj)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[ti][tj][4 * g + j] *= qsv[tj] * sr[j];
+      }
+    char* wl = smem + w * (v4::WQ * v2::EPI_ROWB);
+    v2::stage_acc<bf16, v4::TJ>(acc, wl);
+    __syncthreads();
+    v2::store_staged<bf16, v4::WQ>(wl, a.out, a.out_ld, row0, m_end, rt * v4::TILE + wr * v4::WP, a.R);
+  }
 }
 
 // Per-row absmax fp8 quantisation of a bf16 matrix (one wave per row):
