@@ -133,6 +133,35 @@ int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* 
                       const int32_t* offsets, const int32_t* expert_order, int n_experts, int E_glu,
                       void* out, void* stream);
 
+/* Down-projection dX for fused codes (0 SiLU, 1 ReLU^2) with the combine backward folded in.
+ * For sorted row m of GLU expert e, token t = sorted_token[m], w = top_k_weights[sorted_flat[m]]:
+ * s = grad_out[t] @ down_proj[e] (grad_out rows gathered, grad_out_ld elements apart);
+ * ggu_out[m] = GLU backward of w*s; inter_w_out[m] = w * act(gate)*up (the down weight gradient's
+ * row operand, so grad_eo = w*grad_out is never materialised); wt_partial[p*n_rows + m] = the
+ * partial dot sum over channel slice p of s*inter, p < moe_gate_grad_parts(I).
+ * Replaces moe_combine_bwd + moe_grouped_down_dx_swiglu_bwd for these codes: grad_eo = w*go and
+ * grad_w = <go, eo> = <go @ W_d, inter> (kernels/sm75/moe.py:606-611,712-720). H % 64 == 0,
+ * dtype bf16 or f16. */
+int moe_grouped_down_dx_gated_bwd(int dtype, const void* grad_out, int64_t grad_out_ld,
+                                  const void* down_proj, int E_glu, int64_t H, int64_t I,
+                                  const void* gate_up, const int32_t* act_codes,
+                                  const void* top_k_weights, const int32_t* offsets,
+                                  const int32_t* sorted_token, const int32_t* sorted_flat,
+                                  int64_t n_rows, void* ggu_out, void* inter_w_out,
+                                  float* wt_partial, void* stream);
+
+/* Number of channel slices (rows of wt_partial) moe_grouped_down_dx_gated_bwd writes for I. */
+int moe_gate_grad_parts(int64_t I);
+
+/* Gate-weight gradient from the partials above: grad_wt[t*k+j] = sum_p wt_partial[p*n_rows + pos]
+ * (GLU slot, pos = flat_to_sorted[t*k+j], p ascending), <grad_out[t], hidden[t]> (Identity),
+ * 0 (Zero or invalid index); fp32 accumulation (kernels/sm75/moe.py:712-720). */
+int moe_gate_grad(int dtype, const float* wt_partial, int n_parts, int64_t n_rows,
+                  const void* grad_out, int64_t grad_out_ld, const void* hidden,
+                  const int64_t* top_k_indices, const int32_t* act_codes, int n_experts, int E_glu,
+                  const int32_t* flat_to_sorted, int64_t n_tokens, int top_k, int64_t H,
+                  void* grad_wt_out, void* stream);
+
 /* Un-permute backward: grad_x[t] = sum_j contribution(t,j) in slot order, fp32 accumulation;
  * contribution = grad_xs[flat_to_sorted[t*k+j]] (GLU), w * grad_out[t] (Identity), 0 (Zero).
  * Replaces grad_x.index_add_(0, st, grad_x_s) (kernels/sm75/moe.py:614-615,822) and the Identity

@@ -201,3 +201,24 @@ def test_batched_glu_all_codes():
     assert _rel(y, yr) < 1e-5
     assert _rel(x.grad, xr.grad) < 1e-5
     assert _rel(a_.grad, ar.grad) < 1e-4 and _rel(g_.grad, gr.grad) < 1e-4
+
+
+@pytest.mark.parametrize("needs", ["wt", "down", "gate_up", "hidden"])
+def test_bf16_partial_grads_and_strided_grad_out(needs):
+    """Each leaf alone requiring grad (the backward skips the other products), with grad_out a
+    column slice of a wider tensor so its rows are 384 elements apart."""
+    codes = [0, 1, 0, 1, 3, 4]
+    hid, idx, w, gu, dw, codes_t, ap, go = _case(codes, 4, dtype=torch.bfloat16, n=333, h=256,
+                                                 i=320, k=2, seed=5)
+    _say(f"bf16 partial grads: {needs}")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
+    d = {n: t.cuda() for n, t in zip(("hidden", "wt", "gate_up", "down"), (hid, w, gu, dw))}
+    d[needs].requires_grad_(True)
+    out = kernels.moe(d["hidden"], idx.cuda(), d["wt"], d["gate_up"], d["down"], codes_t.cuda())
+    wide = torch.zeros(hid.shape[0], 384, device="cuda", dtype=torch.bfloat16)
+    wide[:, :256] = go.cuda()
+    out.backward(wide[:, :256])
+    torch.cuda.synchronize()
+    key = {"wt": "grad_wt", "down": "grad_down", "gate_up": "grad_gate_up",
+           "hidden": "grad_hidden"}[needs]
+    _assert_bf16({key: d[needs].grad}, ref, keys=(key,))

@@ -466,6 +466,70 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
         }
       }
     }
+  } else if constexpr (EPI == EPI_GLU_BWD_GATED) {
+    // Staged value = grad_out[t] @ down_proj[e] (no gate). With w = gate of the row, inter =
+    // act(g) * u recomputed in fp32: grad_inter = w * staged, the GLU backward of grad_inter,
+    // gate*inter for the down weight gradient, and the gate gradient's partial dot
+    // sum_ch staged * inter (kernels/sm75/moe.py:712-720: <grad_out, eo> = <grad_out @ W_d, inter>).
+    const int code = a.act_codes ? a.act_codes[e] : 0;
+    const int c = lane & 15;
+    const int ch = rt * v2::TILE + wr * v2::WT + 8 * c;
+    const int chc = min(ch, a.I - 8);
+    const bool cok = ch < a.I;
+    const T* gu = (const T*)a.aux;
+    const T* gw = (const T*)a.gate;
+    T* ggu = (T*)a.out;
+    T* iw = (T*)a.out2;
+    float* part = a.part + (size_t)(2 * rt + wr) * a.out_ld;  // out_ld = M (partials row length)
+    constexpr int NB = 8;  // rows per batch of loads
+#pragma unroll 1
+    for (int i0 = 0; i0 < WQ / 4; i0 += NB) {
+      i32x4 gq[NB], uq[NB];
+      float wv[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int m = min(row0 + (i0 + b) * 4 + (lane >> 4), m_end - 1);
+        const T* r = gu + (size_t)m * 2 * a.I + chc;
+        gq[b] = *(const i32x4*)r;
+        uq[b] = *(const i32x4*)(r + a.I);
+        wv[b] = to_f32(gw[a.sflat[m]]);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int q = (i0 + b) * 4 + (lane >> 4);
+        const int m = row0 + q;
+        const i32x4 oq = v2::staged(wl, q, c);
+        float go[8], gv[8], uv[8], dg[8], du[8], ia[8];
+        v2::unpack8<T>(oq, go);
+        v2::unpack8<T>(gq[b], gv);
+        v2::unpack8<T>(uq[b], uv);
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float act = glu_act(code, gv[j]);
+          const float inter = act * uv[j];
+          dot += cok ? go[j] * inter : 0.f;
+          const float gi = wv[b] * go[j];
+          dg[j] = gi * uv[j] * glu_dact(code, gv[j]);
+          du[j] = gi * act;
+          ia[j] = wv[b] * inter;
+        }
+        // The row's 16 lanes (channels 8c .. 8c+7 each) sum their partial dots.
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) dot += __shfl_xor(dot, d, 64);
+        if (m < m_end) {
+          if (c == 0) part[m] = dot;
+          if (cok) {
+            if (ggu) {
+              T* r = ggu + (size_t)m * 2 * a.I + ch;
+              *(i32x4*)r = v2::pack8<T>(dg);
+              *(i32x4*)(r + a.I) = v2::pack8<T>(du);
+            }
+            if (iw) *(i32x4*)(iw + (size_t)m * a.I + ch) = v2::pack8<T>(ia);
+          }
+        }
+      }
+    }
   } else {  // EPI_GLU_BWD
     const int code = a.act_codes ? a.act_codes[e] : 0;
     const int c = lane & 15;
@@ -948,6 +1012,40 @@ extern "C" int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo,
     case MOE_DT_F16: return go.template operator()<f16>();
     default: return go.template operator()<float>();
   }
+}
+
+extern "C" int moe_gate_grad_parts(int64_t I) { return (int)(2 * ((I + v4::TILE - 1) / v4::TILE)); }
+
+extern "C" int moe_grouped_down_dx_gated_bwd(int dtype, const void* grad_out, int64_t grad_out_ld,
+                                             const void* down_proj, int E_glu, int64_t H,
+                                             int64_t I, const void* gate_up,
+                                             const int32_t* act_codes, const void* top_k_weights,
+                                             const int32_t* offsets, const int32_t* sorted_token,
+                                             const int32_t* sorted_flat, int64_t n_rows,
+                                             void* ggu_out, void* inter_w_out, float* wt_partial,
+                                             void* stream) {
+  if (dtype != MOE_DT_BF16 && dtype != MOE_DT_F16) return MOE_ERR_DTYPE;
+  int st = check_common(dtype, H, I, E_glu, n_rows);
+  if (st) return st;
+  if (H % 64 != 0) return MOE_ERR_ALIGN;
+  if (n_rows == 0) return MOE_OK;
+  if (!grad_out || !down_proj || !gate_up || !act_codes || !top_k_weights || !offsets ||
+      !sorted_token || !sorted_flat || !wt_partial)
+    return MOE_ERR_SHAPE;
+  if (grad_out_ld < H || grad_out_ld % 8 != 0) return MOE_ERR_ALIGN;
+  if (!aligned16(grad_out) || !aligned16(down_proj) || !aligned16(gate_up) ||
+      (ggu_out && !aligned16(ggu_out)) || (inter_w_out && !aligned16(inter_w_out)))
+    return MOE_ERR_ALIGN;
+  TokenArgs a = {};
+  // P[r = i, k = h] = down_proj[e, h, i]: row-contiguous; Q = grad_out rows gathered per token.
+  a.P = down_proj; a.p_e = H * I; a.p_ld = I; a.R = (int)I; a.K = (int)H;
+  a.Q = grad_out; a.q_ld = grad_out_ld; a.q_gather = sorted_token;
+  a.offsets = offsets; a.E_glu = E_glu; a.act_codes = act_codes; a.I = (int)I;
+  a.out = ggu_out; a.out2 = inter_w_out; a.aux = gate_up;
+  a.gate = top_k_weights; a.sflat = sorted_flat; a.part = wt_partial; a.out_ld = n_rows;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == MOE_DT_BF16) return launch_token_v2<bf16, EPI_GLU_BWD_GATED, true>(a, n_rows, s);
+  return launch_token_v2<f16, EPI_GLU_BWD_GATED, true>(a, n_rows, s);
 }
 
 extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj,

@@ -10,7 +10,9 @@ constexpr int MAX_GLU_EXPERTS = 1024;
 constexpr int BK_BYTES = 128;            // bytes of K per LDS row (first-generation kernels)
 constexpr int LDS_ROW = BK_BYTES + 16;   // padded LDS row
 
-enum EpiMode { EPI_STORE = 0, EPI_GLU_FWD = 1, EPI_GLU_BWD = 2 };
+// EPI_GLU_BWD_GATED: as EPI_GLU_BWD, with the token operand = grad_out rows (ungated) and the gate
+// weight applied in the epilogue, which also writes gate * inter and the gate-gradient partials.
+enum EpiMode { EPI_STORE = 0, EPI_GLU_FWD = 1, EPI_GLU_BWD = 2, EPI_GLU_BWD_GATED = 3 };
 
 template <typename T_, int BR_, int BC_, int WR_, int WC_>
 struct Cfg {
@@ -99,8 +101,14 @@ struct TokenArgs {
   int I;              // intermediate size (GLU epilogues)
   void* out;          // EPI_STORE: (M, R); EPI_GLU_FWD: gate_up (M, 2I); EPI_GLU_BWD: ggu (M, 2I)
   long long out_ld;
-  void* out2;         // EPI_GLU_FWD: inter (M, I); EPI_GLU_BWD: grad_inter (M, I)
-  const void* aux;    // EPI_GLU_BWD: gate_up (M, 2I)
+  void* out2;         // EPI_GLU_FWD: inter (M, I); EPI_GLU_BWD: grad_inter (M, I);
+                      // EPI_GLU_BWD_GATED: gate * inter (M, I), may be null
+  const void* aux;    // EPI_GLU_BWD(_GATED): gate_up (M, 2I)
+  // EPI_GLU_BWD_GATED only:
+  const void* gate;        // top_k_weights (N*k), indexed by sorted_flat
+  const int32_t* sflat;    // sorted row -> flat slot t*k+j
+  float* part;             // gate-gradient partials (2 * n_rtiles, M): sum over a wave's 128
+                           // channels of (grad_out @ down_proj) * inter
 };
 
 // Block-wide exclusive scan of the per-expert tile counts into s_pref[0..E]; returns the total.

@@ -193,6 +193,42 @@ combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict_
   if (lane == 0) grad_wt[f] = from_f32<T>(dot);
 }
 
+// Gate gradients from the fused down-dX GEMM: one wave per token; for each routed slot f = t*k+j,
+// GLU expert: grad_wt[f] = sum of the n_parts partial dots of its sorted row (fixed order, so the
+// result is deterministic); Identity: <grad_out[t], hidden[t]>; Zero or invalid: 0
+// (kernels/sm75/moe.py:712-720).
+template <typename T>
+__global__ void __launch_bounds__(ROW_THREADS)
+gate_grad_kernel(const float* __restrict__ part, int n_parts, int64_t n_rows,
+                 const T* __restrict__ go, int64_t go_ld, const T* __restrict__ hidden,
+                 const int64_t* __restrict__ idx, const int32_t* __restrict__ codes, int E_glu,
+                 int E_all, const int32_t* __restrict__ f2s, int64_t N, int k, int H,
+                 T* __restrict__ grad_wt) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
+  if (t >= N) return;
+  const int lane = threadIdx.x & 63;
+  for (int j = 0; j < k; ++j) {
+    const int64_t f = t * k + j;
+    const int pos = f2s[f];
+    const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+    float v = 0.f;
+    if (kind == 0) {
+      for (int p = lane; p < n_parts; p += 64) v += part[(size_t)p * n_rows + pos];
+    } else if (kind == 1) {
+      for (int c = lane * V; c < H; c += 64 * V) {
+        float g[V], x[V];
+        Vec8<T>::ld(go + (size_t)t * go_ld + c, g);
+        Vec8<T>::ld(hidden + (size_t)t * H + c, x);
+#pragma unroll
+        for (int i = 0; i < V; ++i) v += g[i] * x[i];
+      }
+    }
+    v = wave_sum(v);
+    if (lane == 0) grad_wt[f] = from_f32<T>(v);
+  }
+}
+
 // grad_x[t] = sum_j (GLU: grad_xs[pos]; Identity: w*go[t]; Zero: 0)
 template <typename T, int BATCH>
 __global__ void __launch_bounds__(ROW_THREADS)
@@ -443,6 +479,29 @@ extern "C" int moe_combine_bwd(int dtype, const void* grad_out, int64_t grad_out
                (const T_*)grad_out, grad_out_ld, (const T_*)eo, (const T_*)hidden,
                (const T_*)top_k_weights, top_k_indices, act_codes, E_glu, n_experts, sorted_token,
                sorted_flat, n_rows, (int)H, (T_*)grad_eo_out, (T_*)grad_wt_out);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_gate_grad(int dtype, const float* wt_partial, int n_parts, int64_t n_rows,
+                             const void* grad_out, int64_t grad_out_ld, const void* hidden,
+                             const int64_t* top_k_indices, const int32_t* act_codes,
+                             int n_experts, int E_glu, const int32_t* flat_to_sorted,
+                             int64_t n_tokens, int top_k, int64_t H, void* grad_wt_out,
+                             void* stream) {
+  int st = check_rows(dtype, n_tokens, top_k, H, n_experts, E_glu);
+  if (st) return st;
+  if (n_parts < 0 || n_rows < 0) return MOE_ERR_SHAPE;
+  if (n_tokens == 0) return MOE_OK;
+  if (!grad_out || !hidden || !top_k_indices || !act_codes || !flat_to_sorted || !grad_wt_out ||
+      (E_glu > 0 && n_rows > 0 && n_parts > 0 && !wt_partial))
+    return MOE_ERR_SHAPE;
+  if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
+  if (!al16(grad_out) || !al16(hidden)) return MOE_ERR_ALIGN;
+  hipStream_t s = (hipStream_t)stream;
+  MOE_BY_DTYPE(dtype, gate_grad_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
+               wt_partial, n_parts, n_rows, (const T_*)grad_out, grad_out_ld, (const T_*)hidden,
+               top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H,
+               (T_*)grad_wt_out);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 

@@ -31,6 +31,10 @@ _SIGS = {
     "moe_combine_fwd": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_combine_bwd": [_I, _P, _L, _P, _P, _P, _P, _P, _I, _I, _P, _P, _L, _I, _L, _P, _P, _P],
     "moe_grouped_down_dx_swiglu_bwd": [_I, _P, _P, _I, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P],
+    "moe_grouped_down_dx_gated_bwd": [_I, _P, _L, _P, _I, _L, _L, _P, _P, _P, _P, _P, _P, _L,
+                                      _P, _P, _P, _P],
+    "moe_gate_grad_parts": [_L],
+    "moe_gate_grad": [_I, _P, _I, _L, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_grouped_gateup_dx": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
     "moe_grouped_wgrad": [_I, _P, _L, _P, _P, _L, _P, _L, _L, _P, _P, _I, _I, _P, _P],
     "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
@@ -40,7 +44,7 @@ _SIGS = {
     "moe_rowquant_fp8": [_P, _L, _L, _P, _P, _P],
     "moe_mxfp8_fwd": [_P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P],
 }
-_RESTYPES = {"moe_version": ctypes.c_char_p, "moe_get_workspace_size": ctypes.c_size_t}
+_RESTYPES = {"moe_version": ctypes.c_char_p, "moe_gate_grad_parts": ctypes.c_int, "moe_get_workspace_size": ctypes.c_size_t}
 
 _ERRORS = {
     1: (ValueError, "shape"),

@@ -145,6 +145,12 @@ def _row_params(routing, codes_t, ap32, n_experts, m):
     return row_act, row_alpha, row_gamma, rexp
 
 
+def _gated_bwd(fused, e_glu, m, dt, h):
+    """Whether the backward folds the combine backward into the down-dX GEMM (fused codes,
+    16-bit dtypes, H a multiple of the GEMM's 64-wide K step)."""
+    return fused and e_glu > 0 and m > 0 and dt != torch.float32 and h % 64 == 0
+
+
 class _MoEFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, idx, wt, gate_up_proj, down_proj, act_codes, act_params):
@@ -196,8 +202,10 @@ class _MoEFunction(torch.autograd.Function):
                   _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu, _lib.ptr(routing.flat_to_sorted),
                   n_tok, k, h, _lib.ptr(out), stream)
 
+        # The folded backward recomputes <grad_out, eo> from inter, so eo need not stay alive.
+        keep_eo = torch.empty(0) if _gated_bwd(fused, e_glu, m, dt, h) else eo
         ctx.save_for_backward(hidden, idx, wt, gate_up_proj, down_proj, codes_t,
-                              ap32 if ap32 is not None else torch.empty(0), gate_up, inter, eo)
+                              ap32 if ap32 is not None else torch.empty(0), gate_up, inter, keep_eo)
         ctx.routing = routing
         ctx.row = row
         ctx.meta = (n_tok, h, inter_dim, k, e_glu, n_exp, fused, ap32 is not None)
@@ -224,6 +232,9 @@ class _MoEFunction(torch.autograd.Function):
         need_x, need_wt, need_gu, need_dw = (ctx.needs_input_grad[0], ctx.needs_input_grad[2],
                                              ctx.needs_input_grad[3], ctx.needs_input_grad[4])
         need_ap = has_ap and ctx.needs_input_grad[6]
+
+        if _gated_bwd(fused, e_glu, m, dt, h):
+            return _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap)
 
         grad_eo = torch.empty(m, h, device=dev, dtype=dt)
         grad_wt = torch.zeros(n_tok * k, device=dev, dtype=dt)
@@ -294,6 +305,63 @@ class _MoEFunction(torch.autograd.Function):
                       _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu if gxs is not None else 0,
                       _lib.ptr(routing.flat_to_sorted), n_tok, k, h, _lib.ptr(g_x), stream)
         return (g_x, None, grad_wt.view(n_tok, k) if need_wt else None, g_gu, g_dw, None, g_ap)
+
+
+def _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap):
+    """Backward for fused activation codes with the combine backward folded into the down-dX GEMM:
+    grad_eo = w * grad_out is never stored; that GEMM gathers grad_out rows itself, applies w in
+    its epilogue, writes w * inter for the down weight gradient and per-slice partials of the gate
+    gradient <grad_out, eo> = <grad_out @ W_d, inter> (kernels/sm75/moe.py:606-617,712-720)."""
+    (hidden, idx, wt, gate_up_proj, down_proj, codes_t, ap32, gate_up, inter,
+     _eo) = ctx.saved_tensors
+    n_tok, h, inter_dim, k, e_glu, n_exp, _fused, _has_ap = ctx.meta
+    routing = ctx.routing
+    dt = hidden.dtype
+    dtc = _lib.dtype_code(dt)
+    dev = hidden.device
+    stream = _lib.stream_of(dev)
+    m = n_tok * k
+    go_ld = go.stride(0)
+    if not (need_x or need_wt or need_gu or need_dw):
+        return (None, None, None, None, None, None, torch.zeros_like(ap32) if need_ap else None)
+    n_parts = _lib.lib().moe_gate_grad_parts(inter_dim)
+    part = torch.empty(n_parts, m, device=dev, dtype=torch.float32)
+    ggu = torch.empty(m, 2 * inter_dim, device=dev, dtype=dt) if (need_x or need_gu) else None
+    inter_w = torch.empty(m, inter_dim, device=dev, dtype=dt) if need_dw else None
+    _lib.call("moe_grouped_down_dx_gated_bwd", dtc, _lib.ptr(go), go_ld, _lib.ptr(down_proj),
+              e_glu, h, inter_dim, _lib.ptr(gate_up), _lib.ptr(codes_t), _lib.ptr(wt),
+              _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token),
+              _lib.ptr(routing.sorted_flat), m, _lib.ptr(ggu), _lib.ptr(inter_w), _lib.ptr(part),
+              stream)
+    g_wt = g_dw = g_gu = g_x = None
+    if need_wt:
+        g_wt = torch.empty(n_tok, k, device=dev, dtype=dt)
+        _lib.call("moe_gate_grad", dtc, _lib.ptr(part), n_parts, m, _lib.ptr(go), go_ld,
+                  _lib.ptr(hidden), _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu,
+                  _lib.ptr(routing.flat_to_sorted), n_tok, k, h, _lib.ptr(g_wt), stream)
+    if need_dw:
+        g_dw = torch.empty_like(down_proj)
+        _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(inter_w), inter_dim, None, _lib.ptr(go),
+                  go_ld, _lib.ptr(routing.sorted_token), inter_dim, h, _lib.ptr(routing.offsets),
+                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw), stream,
+                  tag="down")
+    if need_gu:
+        g_gu = torch.empty_like(gate_up_proj)
+        _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(hidden), h, _lib.ptr(routing.sorted_token),
+                  _lib.ptr(ggu), 2 * inter_dim, None, h, 2 * inter_dim, _lib.ptr(routing.offsets),
+                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_gu), stream,
+                  tag="gate_up")
+    if need_x:
+        gxs = torch.empty(m, h, device=dev, dtype=dt)
+        _lib.call("moe_grouped_gateup_dx", dtc, _lib.ptr(ggu), _lib.ptr(gate_up_proj), e_glu, h,
+                  inter_dim, _lib.ptr(routing.offsets), _lib.ptr(routing.tile_offsets), m,
+                  _lib.ptr(gxs), stream)
+        g_x = torch.empty(n_tok, h, device=dev, dtype=dt)
+        _lib.call("moe_unpermute_bwd", dtc, _lib.ptr(gxs), _lib.ptr(go), go_ld, _lib.ptr(wt),
+                  _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu, _lib.ptr(routing.flat_to_sorted),
+                  n_tok, k, h, _lib.ptr(g_x), stream)
+    g_ap = torch.zeros_like(ap32) if need_ap else None
+    return (g_x, None, g_wt, g_gu, g_dw, None, g_ap)
 
 
 def moe_per_expert(hidden, top_k_indices, top_k_weights, gate_up_proj, down_proj, act_codes,
