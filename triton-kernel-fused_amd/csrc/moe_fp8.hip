@@ -136,7 +136,7 @@ fp8_gemm_kernel(Fp8Args a, int n_logical) {
     for (int it = 0; it < v4::WQ / 8; ++it) {
       const int q = it * 8 + (lane >> 3);
       const i32x4 v = *(const i32x4*)(wl + q * 128 + ((c ^ (q & 7)) << 4));
-      if (row0 + q < m_end && ch < a.I) *(i32x4*)(a.out + (size_t)(row0 + q) * a.I + ch) = v;
+      if (row0 + q < m_end && ch < a.I) v2::st_stream(v, a.out + (size_t)(row0 + q) * a.I + ch);
     }
   } else {
 #pragma unroll

@@ -454,15 +454,15 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
       const i32x4 gq = v2::staged(wl, q, c), uq = v2::staged(wl, q, c + 8);
       if (m < m_end && ch < a.I) {
         T* r = gu + (size_t)m * 2 * a.I + ch;
-        *(i32x4*)r = gq;
-        *(i32x4*)(r + a.I) = uq;
+        v2::st_stream(gq, r);
+        v2::st_stream(uq, r + a.I);
         if (it) {
           float gv[8], uv[8], iv[8];
           v2::unpack8<T>(gq, gv);
           v2::unpack8<T>(uq, uv);
 #pragma unroll
           for (int j = 0; j < 8; ++j) iv[j] = glu_act(code, gv[j]) * uv[j];
-          *(i32x4*)(it + (size_t)m * a.I + ch) = v2::pack8<T>(iv);
+          v2::st_stream(v2::pack8<T>(iv), it + (size_t)m * a.I + ch);
         }
       }
     }
@@ -522,10 +522,10 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
           if (cok) {
             if (ggu) {
               T* r = ggu + (size_t)m * 2 * a.I + ch;
-              *(i32x4*)r = v2::pack8<T>(dg);
-              *(i32x4*)(r + a.I) = v2::pack8<T>(du);
+              v2::st_stream(v2::pack8<T>(dg), r);
+              v2::st_stream(v2::pack8<T>(du), r + a.I);
             }
-            if (iw) *(i32x4*)(iw + (size_t)m * a.I + ch) = v2::pack8<T>(ia);
+            if (iw) v2::st_stream(v2::pack8<T>(ia), iw + (size_t)m * a.I + ch);
           }
         }
       }
@@ -557,7 +557,7 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
         const int m = row0 + q;
         const i32x4 oq = v2::staged(wl, q, c);
         if (m < m_end && ch < a.I) {
-          if (gi) *(i32x4*)(gi + (size_t)m * a.I + ch) = oq;
+          if (gi) v2::st_stream(oq, gi + (size_t)m * a.I + ch);
           if (ggu) {
             float go[8], gv[8], uv[8], dg[8], du[8];
             v2::unpack8<T>(oq, go);
@@ -569,8 +569,8 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
               du[j] = go[j] * glu_act(code, gv[j]);
             }
             T* r = ggu + (size_t)m * 2 * a.I + ch;
-            *(i32x4*)r = v2::pack8<T>(dg);
-            *(i32x4*)(r + a.I) = v2::pack8<T>(du);
+            v2::st_stream(v2::pack8<T>(dg), r);
+            v2::st_stream(v2::pack8<T>(du), r + a.I);
           }
         }
       }

@@ -277,6 +277,13 @@ __device__ __forceinline__ i32x4 staged(const char* wl, int q, int c) {
   return *(const i32x4*)(wl + staged_off(q, c));
 }
 
+// GEMM outputs are written once and read by a later kernel: stored nontemporal so they do not
+// displace operand lines in L2 (measured 1-3% faster on the 256x256 GEMMs).
+template <typename P>
+__device__ __forceinline__ void st_stream(i32x4 v, P* p) {
+  __builtin_nontemporal_store(v, (i32x4*)p);
+}
+
 // Plain store of a staged block of WQ rows: out row (row0 + q) gets channels ch0 + 8c .. +7 for
 // the rows below row_end and channels below n_ch (a multiple of 8).
 template <typename T, int WQ = WT>
@@ -288,7 +295,7 @@ __device__ __forceinline__ void store_staged(const char* wl, T* out, long long l
   for (int it = 0; it < WQ / 4; ++it) {
     const int q = it * 4 + (lane >> 4);
     const i32x4 v = staged(wl, q, c);
-    if (row0 + q < row_end && ch < n_ch) *(i32x4*)(out + (size_t)(row0 + q) * ld + ch) = v;
+    if (row0 + q < row_end && ch < n_ch) st_stream(v, out + (size_t)(row0 + q) * ld + ch);
   }
 }
 
