@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 # algorithmic FLOPs per call of each entry point, in units of M*H*I (M = routed GLU rows)
 KERNEL_MHI = {
     "moe_grouped_gateup_swiglu_fwd": 4, "moe_grouped_down_fwd": 2,
-    "moe_grouped_down_dx_swiglu_bwd": 2, "moe_grouped_gateup_dx": 4,
+    "moe_grouped_down_dx_swiglu_bwd": 2, "moe_grouped_down_dx_gated_bwd": 2, "moe_grouped_gateup_dx": 4,
     "moe_grouped_wgrad:down": 2, "moe_grouped_wgrad:gate_up": 4,
 }
 
