@@ -8,8 +8,8 @@
 // contiguous weight bytes of one row per 128-byte K chunk (the two lane halves cover the chunk,
 // so every row read is a whole 128-byte line), converts them to bf16 with
 // v_cvt_scalef32_pk_bf16_fp8 (the block scale 2^(s-127) applied in the conversion, exact in
-// bf16), and feeds v_mfma_f32_32x32x16_bf16 with the expert's tokens as the other operand
-// (token rows read from L2: decode batches are small). The four partial accumulators are summed
+// bf16), and feeds v_mfma_f32_16x16x32_bf16 with the expert's tokens as the other operand
+// (token rows staged in LDS: decode batches are small). The four partial accumulators are summed
 // through LDS; the gate/up kernel applies SwiGLU and writes the bf16 intermediate, the down
 // kernel writes the expert outputs, and the gate-weighted combine (moe_combine_fwd) finishes.
 #include "moe_gemm_common.h"
@@ -83,6 +83,7 @@ __host__ __device__ inline int mx_x_offset(int nc, int rt) {
 template <bool GLU, int RT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
+  static_assert(RT == 1 || RT == 2, "row tiles per block");
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int ng = (a.n_rtiles + RT - 1) / RT;
   const int e = (int)blockIdx.x / ng;
@@ -95,11 +96,15 @@ mx_gemm_kernel(MxArgs a) {
   const int rr = lane & 15, q = lane >> 4;
   const int nc = a.K / 128;
   const int c_begin = w * nc / MX_WAVES, c_end = (w + 1) * nc / MX_WAVES;
+  const int nch = c_end - c_begin;  // >= 1: K is a multiple of 512
+  const int total = nrt * nch;      // (tile, chunk) items of this wave, tile-major
   const int sw = mx_scale_words(nc);
   auto stab_of = [&](int j) { return (uint32_t*)lds + (j * MX_WAVES + w) * MX_ROWS * sw; };
   char* xlds = lds + mx_x_offset(nc, RT);
   f32x4* red = (f32x4*)(RT > 1 ? lds + mx_table_bytes(nc, RT) : xlds);
   const int x_bytes = MX_LDS - mx_x_offset(nc, RT);
+  // Block barrier without HIP's release fence: weight loads stay in flight across it.
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
   // Weight row i of tile rt (clamped into the matrix; rows outside it feed unstored outputs).
   auto wrow = [&](int rt, int i) {
@@ -109,7 +114,38 @@ mx_gemm_kernel(MxArgs a) {
     }
     return min(rt * MX_ROWS + i, a.R - 1);
   };
-  // Scale tables: row i of tile j, this wave's chunks.
+  // This lane's four weight rows of tile 0 and tile 1 of the block (tile 1 = tile 0 if absent).
+  const uint8_t* wp0[4];
+  const uint8_t* wp1[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    wp0[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt0, 16 * t + rr) * a.w_ld + 16 * q;
+    wp1[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt0 + (nrt > 1), 16 * t + rr) * a.w_ld + 16 * q;
+  }
+
+  // Two register buffers of weight bytes (no copies): item i+1 is in flight while item i
+  // computes, and across tile ends the next tile's first chunk is in flight during the partial-sum
+  // exchange and the epilogue. Fetches past the last item re-read it (every path has the same
+  // loads in flight, so the compiler's waits stay partial).
+  struct Buf { uint4 v[4][2]; };
+  Buf p0, p1;
+  int fj = 0, fc = c_begin;  // next item to fetch
+  auto fetch = [&](Buf& f) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint8_t* r = (fj ? wp1[t] : wp0[t]) + fc * 128;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) f.v[t][jj] = *(const uint4*)(r + 64 * jj);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (++fc == c_end) {
+      if (fj + 1 < nrt) { ++fj; fc = c_begin; }
+      else fc = c_end - 1;
+    }
+  };
+
+  // The first weight chunk goes out before the scale tables and token rows are staged.
+  fetch(p0);
   {
     const int nw = c_end - c_begin;
     for (int j = 0; j < nrt; ++j) {
@@ -125,11 +161,16 @@ mx_gemm_kernel(MxArgs a) {
   for (int mb = m_begin; mb < m_end; mb += MX_TOK) {
     const int nt = min(MX_TOK, m_end - mb);
     const int m = mb + rr;
+    if (mb != m_begin) {
+      fj = 0;
+      fc = c_begin;
+      fetch(p0);
+    }
     // Token rows: staged in LDS when they fit (a decode batch gives an expert a handful), else
     // read from L2 per chunk. Lanes past the last token read the last token's row: they only
     // feed output columns that are never stored.
     const bool x_lds = (size_t)nt * a.K * sizeof(bf16) <= (size_t)x_bytes;
-    __syncthreads();  // scale tables written; the previous token block is done with the LDS
+    barrier();  // scale tables written; the previous token block is done with the LDS
     if (x_lds) {
       const int units = a.K / 8;  // 16-byte units per token row
       for (int u = threadIdx.x; u < nt * units; u += blockDim.x) {
@@ -139,118 +180,109 @@ mx_gemm_kernel(MxArgs a) {
         *(i32x4*)(xlds + ((size_t)tt * a.K + 8 * o) * sizeof(bf16)) =
             ldg16(a.X + (size_t)gr * a.x_ld + 8 * o);
       }
-      __syncthreads();
+      barrier();
     }
     const int mt = mb + min(rr, nt - 1);
     const int xr = a.x_gather ? a.x_gather[mt] : mt;
     const bf16* xrow = a.X + (size_t)xr * a.x_ld;
     const char* xl = xlds + (size_t)min(rr, nt - 1) * a.K * sizeof(bf16);
 
-    for (int j = 0; j < nrt; ++j) {
-      const int rt = rt0 + j;
-      const uint32_t* stab = stab_of(j);
-      const uint8_t* wp[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        wp[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt, 16 * t + rr) * a.w_ld + 16 * q;
+    auto run = [&](auto xl_c) {
+      constexpr bool XL = decltype(xl_c)::value;
       f32x4 acc[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-      // Two register buffers of weight bytes (no copies): chunk c+1 is in flight while chunk c
-      // computes; the prefetch is unconditional (the last one re-reads a valid chunk) so every
-      // path has the same loads in flight and the compiler's waits stay partial.
-      auto kloop = [&](auto xl_c) {
-        constexpr bool XL = decltype(xl_c)::value;
-        struct Buf { uint4 v[4][2]; };
-        Buf p0, p1;
-        auto fetch = [&](int c, Buf& f) {
+      int cj = 0, cc = c_begin;  // item being computed
+      auto compute = [&](const Buf& f) {
+        i32x4 xv[4];  // token fragments of the four K steps
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
+        for (int ks = 0; ks < 4; ++ks) {
+          const int k = cc * 128 + (ks >> 1) * 64 + 16 * q + 8 * (ks & 1);
+          if constexpr (XL) xv[ks] = *(const i32x4*)(xl + k * sizeof(bf16));
+          else xv[ks] = ldg16(xrow + k);
+        }
+        const uint32_t* stab = stab_of(cj);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) f.v[t][jj] = *(const uint4*)(wp[t] + c * 128 + 64 * jj);
-          __builtin_amdgcn_sched_barrier(0);
-        };
-        auto compute = [&](const Buf& f, int c) {
-          i32x4 xv[4];  // token fragments of the four K steps
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t sc = stab[(16 * t + rr) * sw + (cc - c_begin)];
+          const float s0 = e8m0_to_f32((sc >> (8 * (q >> 1))) & 0xff);
+          const float s1 = e8m0_to_f32((sc >> (8 * (2 + (q >> 1)))) & 0xff);
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) {
-            const int k = c * 128 + (ks >> 1) * 64 + 16 * q + 8 * (ks & 1);
-            if constexpr (XL) xv[ks] = *(const i32x4*)(xl + k * sizeof(bf16));
-            else xv[ks] = ldg16(xrow + k);
-          }
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t sc = stab[(16 * t + rr) * sw + (c - c_begin)];
-            const float s0 = e8m0_to_f32((sc >> (8 * (q >> 1))) & 0xff);
-            const float s1 = e8m0_to_f32((sc >> (8 * (2 + (q >> 1)))) & 0xff);
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-              const uint4 u = f.v[t][ks >> 1];
-              const i32x4 av = (ks & 1) ? dequant8(u.z, u.w, (ks >> 1) ? s1 : s0)
-                                        : dequant8(u.x, u.y, (ks >> 1) ? s1 : s0);
-              acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
-                                                               __builtin_bit_cast(bf16x8, xv[ks]),
-                                                               acc[t], 0, 0, 0);
-            }
-          }
-        };
-        const int c_last = c_end - 1;
-        if (c_begin <= c_last) {
-          fetch(c_begin, p0);
-          for (int c = c_begin; c <= c_last; c += 2) {
-            fetch(min(c + 1, c_last), p1);
-            compute(p0, c);
-            if (c + 1 > c_last) break;
-            fetch(min(c + 2, c_last), p0);
-            compute(p1, c + 1);
+            const uint4 u = f.v[t][ks >> 1];
+            const i32x4 av = (ks & 1) ? dequant8(u.z, u.w, (ks >> 1) ? s1 : s0)
+                                      : dequant8(u.x, u.y, (ks >> 1) ? s1 : s0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                             __builtin_bit_cast(bf16x8, xv[ks]),
+                                                             acc[t], 0, 0, 0);
           }
         }
       };
-      if (x_lds) kloop(std::true_type{});
-      else kloop(std::false_type{});
-
-      // Partial sums of waves 1-3 meet wave 0's in LDS.
-      if (RT == 1) __syncthreads();  // the exchange reuses the token rows' space
-      if (w > 0) {
+      // After the last chunk of tile cj: partial sums of waves 1-3 meet wave 0's in LDS, wave 0
+      // stores the tile.
+      auto finish_tile = [&]() {
+        if (RT == 1) barrier();  // the exchange reuses the token rows' space
+        if (w > 0) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
-      }
-      __syncthreads();
-      if (w == 0) {
+          for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
+        }
+        barrier();
+        if (w == 0) {
 #pragma unroll
-        for (int v = 1; v < MX_WAVES; ++v)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const f32x4 p = red[(v * 4 + t) * 64 + lane];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) acc[t][jj] += p[jj];
-          }
-        // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
-        if (rr < nt) {
-          bf16* o = a.out + (size_t)m * a.out_ld;
-          if (GLU) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const int ch = rt * 32 + 16 * t + 4 * q;
-              if (ch < a.I) {
-                float iv[4];
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) iv[jj] = silu(acc[t][jj]) * acc[t + 2][jj];
-                Store4<bf16>::st(o + ch, iv[0], iv[1], iv[2], iv[3]);
-              }
-            }
-          } else {
+          for (int v = 1; v < MX_WAVES; ++v)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              const int row = rt * MX_ROWS + 16 * t + 4 * q;
-              if (row < a.R) Store4<bf16>::st(o + row, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+              const f32x4 p = red[(v * 4 + t) * 64 + lane];
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) acc[t][jj] += p[jj];
+            }
+          const int rt = rt0 + cj;
+          // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
+          if (rr < nt) {
+            bf16* o = a.out + (size_t)m * a.out_ld;
+            if (GLU) {
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                const int ch = rt * 32 + 16 * t + 4 * q;
+                if (ch < a.I) {
+                  float iv[4];
+#pragma unroll
+                  for (int jj = 0; jj < 4; ++jj) iv[jj] = silu(acc[t][jj]) * acc[t + 2][jj];
+                  Store4<bf16>::st(o + ch, iv[0], iv[1], iv[2], iv[3]);
+                }
+              }
+            } else {
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                const int row = rt * MX_ROWS + 16 * t + 4 * q;
+                if (row < a.R) Store4<bf16>::st(o + row, acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+              }
             }
           }
         }
+        if (RT > 1) barrier();  // wave 0 has read the exchange before the next tile writes it
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      };
+      auto advance = [&]() {
+        if (++cc == c_end) {
+          finish_tile();
+          ++cj;
+          cc = c_begin;
+        }
+      };
+      for (int it = 0; it < total; it += 2) {
+        fetch(p1);
+        compute(p0);
+        advance();
+        if (it + 1 >= total) break;
+        fetch(p0);
+        compute(p1);
+        advance();
       }
-      if (RT > 1) __syncthreads();  // wave 0 has read the exchange before the next tile writes it
-    }
+    };
+    if (x_lds) run(std::true_type{});
+    else run(std::false_type{});
   }
 }
 
