@@ -83,7 +83,6 @@ __host__ __device__ inline int mx_x_offset(int nc, int rt) {
 template <bool GLU, int RT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
-  static_assert(RT == 1 || RT == 2, "row tiles per block");
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int ng = (a.n_rtiles + RT - 1) / RT;
   const int e = (int)blockIdx.x / ng;
@@ -114,14 +113,22 @@ mx_gemm_kernel(MxArgs a) {
     }
     return min(rt * MX_ROWS + i, a.R - 1);
   };
-  // This lane's four weight rows of tile 0 and tile 1 of the block (tile 1 = tile 0 if absent).
-  const uint8_t* wp0[4];
-  const uint8_t* wp1[4];
+  // This lane's four weight rows of tile j: tile 0's rows advanced by j tiles, clamped into the
+  // matrix (gate/up: 32 channels per tile in each half; down: 64 rows).
+  int wr0[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    wp0[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt0, 16 * t + rr) * a.w_ld + 16 * q;
-    wp1[t] = a.W + (size_t)e * a.w_e + (size_t)wrow(rt0 + (nrt > 1), 16 * t + rr) * a.w_ld + 16 * q;
+    const int i = 16 * t + rr;
+    wr0[t] = GLU ? rt0 * 32 + 16 * ((i >> 4) & 1) + (i & 15) : rt0 * MX_ROWS + i;
   }
+  const uint8_t* wbase = a.W + (size_t)e * a.w_e + 16 * q;
+  auto wptr = [&](int j, int t) {
+    if (GLU) {
+      const int ch = min(wr0[t] + 32 * j, a.I - 1);
+      return wbase + (size_t)((t < 2 ? 0 : a.I) + ch) * a.w_ld;
+    }
+    return wbase + (size_t)min(wr0[t] + MX_ROWS * j, a.R - 1) * a.w_ld;
+  };
 
   // Two register buffers of weight bytes (no copies): item i+1 is in flight while item i
   // computes, and across tile ends the next tile's first chunk is in flight during the partial-sum
@@ -133,7 +140,7 @@ mx_gemm_kernel(MxArgs a) {
   auto fetch = [&](Buf& f) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint8_t* r = (fj ? wp1[t] : wp0[t]) + fc * 128;
+      const uint8_t* r = wptr(fj, t) + fc * 128;
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) f.v[t][jj] = *(const uint4*)(r + 64 * jj);
     }
