@@ -216,6 +216,30 @@ int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, const void* w
                   const int32_t* offsets, const int32_t* sorted_token, int64_t n_rows, void* inter,
                   void* eo, void* stream);
 
+/* Router epilogue forward (the fused epilogue of kernels/sm75/router.py:40-103,110-127): for
+ * each token row n of logits (N,E; rows ld elements apart; dtype f32/f16/bf16): scores s =
+ * sigmoid(logits) (softmax = 0) or softmax over the E experts (softmax = 1); selection on s + bias
+ * (bias fp32 (E) or NULL; selection only); top_k picks in descending order, ties to the lower
+ * expert; w = s at the picks, divided by (sum + 1e-20) when norm, times scale. Writes idx_out
+ * (N,top_k) int64 and w_out (N,top_k) fp32; when counts (E) int32 is non-NULL the picks per expert
+ * are added to it (the caller zeroes it). E <= 1024, top_k <= min(32, E). */
+int moe_router_topk_fwd(int dtype, const void* logits, int64_t ld, int64_t n_tokens, int n_experts,
+                        const float* bias, int top_k, int softmax, int norm, float scale,
+                        int64_t* idx_out, float* w_out, int32_t* counts, void* stream);
+
+/* Router epilogue backward (kernels/sm75/router.py:105-150): grad_logits (N,E), rows out_ld
+ * apart, in the logits dtype, from grad_w (N,top_k) fp32 and the forward's idx; the picked raw
+ * scores are recomputed from the logits. */
+int moe_router_topk_bwd(int dtype, const void* logits, int64_t ld, int64_t n_tokens, int n_experts,
+                        const int64_t* idx, const float* grad_w, int top_k, int softmax, int norm,
+                        float scale, void* grad_logits_out, int64_t out_ld, void* stream);
+
+/* Auxiliary-loss-free bias update, in place: bias[e] += u * sign(mean(counts) - counts[e]) in
+ * fp32; no-op for u <= 0. counts must already be the global load
+ * (replaces router_bias_update, kernels/sm75/router.py:293-301). */
+int moe_router_bias_update(float* bias, const int32_t* counts, int n_experts, float u,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

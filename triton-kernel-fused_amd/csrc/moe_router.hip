@@ -1,0 +1,288 @@
+// Router epilogue: the step between the router logits (N, E) and dispatch. Scores (sigmoid or
+// softmax over the experts), selection on scores + bias (bias only steers the choice), top-k, the
+// unbiased scores gathered at the picks, optional sum-to-1 normalisation, routed scaling, and the
+// per-expert pick counts for auxiliary-loss-free load balancing; its backward; and the bias update
+// (kernels/sm75/router.py:40-150,152-170,293-301).
+//
+// One wave owns one token row: lane l holds experts l, l+64, ... (EJ per lane), so a top-k step is
+// a per-lane argmax over its EJ values and a 6-step butterfly over the wave that carries
+// (selection value, expert, score). Ties pick the lowest expert index. Counts are summed per
+// workgroup in LDS and added to the global counters with one integer atomic per expert, so the
+// totals do not depend on the order of the atomics.
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int RT_THREADS = 256;  // 4 waves = 4 token rows per workgroup
+constexpr int RT_MAX_E = 1024;
+constexpr int RT_MAX_K = 32;
+
+__device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Wave butterfly: the larger selection value wins, ties go to the lower expert index.
+__device__ __forceinline__ void argmax_wave(float& v, int& e, float& s) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ov = __shfl_xor(v, d, 64);
+    const int oe = __shfl_xor(e, d, 64);
+    const float os = __shfl_xor(s, d, 64);
+    if (ov > v || (ov == v && oe < e)) {
+      v = ov;
+      e = oe;
+      s = os;
+    }
+  }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// Scores of this lane's experts for one row (invalid experts: score 0).
+template <typename T, int EJ>
+__device__ __forceinline__ void row_scores(const T* row, int E, int softmax, int lane, float (&s)[EJ]) {
+  float x[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = lane + 64 * j;
+    x[j] = e < E ? to_f32(row[e]) : -INFINITY;
+  }
+  if (softmax) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) m = fmaxf(m, x[j]);
+    m = wave_max(m);
+    float z = 0.f;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      s[j] = lane + 64 * j < E ? expf(x[j] - m) : 0.f;
+      z += s[j];
+    }
+    z = wave_add(z);
+    const float rz = 1.0f / z;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) s[j] *= rz;
+  } else {
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) s[j] = lane + 64 * j < E ? sigmoid_acc(x[j]) : 0.f;
+  }
+}
+
+template <typename T, int EJ>
+__global__ void __launch_bounds__(RT_THREADS)
+router_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
+                  const float* __restrict__ bias, int top_k, int softmax, int norm, float scale,
+                  int64_t* __restrict__ idx_out, float* __restrict__ w_out,
+                  int32_t* __restrict__ counts) {
+  __shared__ int s_cnt[RT_MAX_E];
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
+  if (counts) {
+    for (int e = threadIdx.x; e < E; e += RT_THREADS) s_cnt[e] = 0;
+    __syncthreads();
+  }
+  if (n < N) {
+    float s[EJ], sel[EJ];
+    row_scores<T, EJ>(logits + n * ld, E, softmax, lane, s);
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const int e = lane + 64 * j;
+      sel[j] = e < E ? s[j] + (bias ? bias[e] : 0.f) : -INFINITY;
+    }
+    // Lane k keeps pick k (every lane sees the same winner after the butterfly).
+    float my_w = 0.f, tsum = 0.f;
+    int my_e = 0;
+#pragma unroll 1
+    for (int k = 0; k < top_k; ++k) {
+      // This lane's best (first maximum in expert order), then the wave's.
+      float v = -INFINITY, sc = 0.f;
+      int e = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < EJ; ++j)
+        if (sel[j] > v) {
+          v = sel[j];
+          e = lane + 64 * j;
+          sc = s[j];
+        }
+      argmax_wave(v, e, sc);
+#pragma unroll
+      for (int j = 0; j < EJ; ++j)
+        if (lane + 64 * j == e) sel[j] = -INFINITY;
+      if (lane == k) {
+        my_w = sc;
+        my_e = e;
+      }
+      tsum += sc;
+    }
+    const float f = norm ? scale / (tsum + 1e-20f) : scale;
+    if (lane < top_k) {
+      idx_out[n * top_k + lane] = my_e;
+      w_out[n * top_k + lane] = my_w * f;
+      if (counts) atomicAdd(&s_cnt[my_e], 1);
+    }
+  }
+  if (counts) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += RT_THREADS)
+      if (s_cnt[e]) atomicAdd(&counts[e], s_cnt[e]);
+  }
+}
+
+// grad_logits[n, e] from grad_w (fp32, (N, k)): with picked raw scores w_k and T = sum w_k + 1e-20,
+// the scattered score gradient is g_e = sum_{k: idx_k = e} G'_k with G'_k = scale/T (G_k - <G,w>/T)
+// (normalised) or scale G_k; sigmoid: grad = g_e s_e (1 - s_e); softmax: s_e (g_e - sum_k G'_k w_k)
+// (kernels/sm75/router.py:105-150).
+template <typename T, int EJ>
+__global__ void __launch_bounds__(RT_THREADS)
+router_bwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
+                  const int64_t* __restrict__ idx, const float* __restrict__ gw, int top_k,
+                  int softmax, int norm, float scale, T* __restrict__ gout, int64_t gout_ld) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
+  if (n >= N) return;
+  float s[EJ];
+  row_scores<T, EJ>(logits + n * ld, E, softmax, lane, s);
+  // Lane k (< top_k) holds slot k: its expert, upstream gradient and raw picked score.
+  int ek = -1;
+  float gk = 0.f, wk = 0.f;
+  if (lane < top_k) {
+    ek = (int)idx[n * top_k + lane];
+    gk = gw[n * top_k + lane];
+  }
+  // Raw score of expert ek lives in lane ek % 64, slot ek / 64.
+  {
+    const int src = ek >= 0 ? (ek & 63) : 0, jj = ek >= 0 ? (ek >> 6) : 0;
+    float mine = 0.f;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      const float o = __shfl(s[j], src, 64);
+      if (j == jj) mine = o;
+    }
+    wk = ek >= 0 ? mine : 0.f;
+  }
+  float gp;
+  if (norm) {
+    const float t = wave_add(wk) + 1e-20f;
+    const float dot = wave_add(gk * wk);
+    gp = scale / t * (gk - dot / t);
+  } else {
+    gp = scale * gk;
+  }
+  if (ek < 0) gp = 0.f;
+  const float gs = softmax ? wave_add(gp * wk) : 0.f;
+  float g[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) g[j] = 0.f;
+  for (int k = 0; k < top_k; ++k) {
+    const int e = __shfl(ek, k, 64);
+    const float v = __shfl(gp, k, 64);
+#pragma unroll
+    for (int j = 0; j < EJ; ++j)
+      if (lane + 64 * j == e) g[j] += v;
+  }
+  T* orow = gout + n * gout_ld;
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      const float r = softmax ? s[j] * (g[j] - gs) : g[j] * s[j] * (1.f - s[j]);
+      orow[e] = from_f32<T>(r);
+    }
+  }
+}
+
+// bias[e] += u * sign(mean(counts) - counts[e]) in fp32, one workgroup.
+__global__ void __launch_bounds__(1024) router_bias_kernel(float* bias, const int32_t* counts, int E, float u) {
+  __shared__ float s_part[16];
+  float acc = 0.f;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) acc += (float)counts[e];
+  acc = wave_add(acc);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += s_part[i];
+  const float mean = tot / (float)E;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const float d = mean - (float)counts[e];
+    const float sg = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
+    bias[e] += u * sg;
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+static int ej_of(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16; }
+
+#define RT_DISPATCH(dtype, EJV, KERNEL, GRID, STREAM, ...)                                   \
+  do {                                                                                       \
+    auto launch = [&]<typename T_>() {                                                       \
+      switch (EJV) {                                                                         \
+        case 1: hipLaunchKernelGGL((KERNEL<T_, 1>), GRID, dim3(RT_THREADS), 0, STREAM, __VA_ARGS__); break; \
+        case 2: hipLaunchKernelGGL((KERNEL<T_, 2>), GRID, dim3(RT_THREADS), 0, STREAM, __VA_ARGS__); break; \
+        case 4: hipLaunchKernelGGL((KERNEL<T_, 4>), GRID, dim3(RT_THREADS), 0, STREAM, __VA_ARGS__); break; \
+        case 8: hipLaunchKernelGGL((KERNEL<T_, 8>), GRID, dim3(RT_THREADS), 0, STREAM, __VA_ARGS__); break; \
+        default: hipLaunchKernelGGL((KERNEL<T_, 16>), GRID, dim3(RT_THREADS), 0, STREAM, __VA_ARGS__); break; \
+      }                                                                                      \
+    };                                                                                       \
+    if ((dtype) == MOE_DT_BF16) launch.template operator()<bf16>();                          \
+    else if ((dtype) == MOE_DT_F16) launch.template operator()<f16>();                       \
+    else launch.template operator()<float>();                                                \
+  } while (0)
+
+static int check_router(int dtype, int64_t N, int E, int top_k, int64_t ld) {
+  if (dtype != MOE_DT_F32 && dtype != MOE_DT_F16 && dtype != MOE_DT_BF16) return MOE_ERR_DTYPE;
+  if (N < 0 || N >= ((int64_t)1 << 31) / 4 || E <= 0 || E > RT_MAX_E || top_k <= 0 ||
+      top_k > RT_MAX_K || top_k > E || ld < E)
+    return MOE_ERR_SHAPE;
+  return MOE_OK;
+}
+
+extern "C" int moe_router_topk_fwd(int dtype, const void* logits, int64_t ld, int64_t n_tokens,
+                                   int n_experts, const float* bias, int top_k, int softmax,
+                                   int norm, float scale, int64_t* idx_out, float* w_out,
+                                   int32_t* counts, void* stream) {
+  int st = check_router(dtype, n_tokens, n_experts, top_k, ld);
+  if (st) return st;
+  if (n_tokens == 0) return MOE_OK;
+  if (!logits || !idx_out || !w_out) return MOE_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((n_tokens + 3) / 4));
+  RT_DISPATCH(dtype, ej_of(n_experts), router_fwd_kernel, grid, s, (const T_*)logits, ld, n_tokens,
+              n_experts, bias, top_k, softmax, norm, scale, idx_out, w_out, counts);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_router_topk_bwd(int dtype, const void* logits, int64_t ld, int64_t n_tokens,
+                                   int n_experts, const int64_t* idx, const float* grad_w,
+                                   int top_k, int softmax, int norm, float scale,
+                                   void* grad_logits_out, int64_t out_ld, void* stream) {
+  int st = check_router(dtype, n_tokens, n_experts, top_k, ld);
+  if (st) return st;
+  if (out_ld < n_experts) return MOE_ERR_SHAPE;
+  if (n_tokens == 0) return MOE_OK;
+  if (!logits || !idx || !grad_w || !grad_logits_out) return MOE_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((n_tokens + 3) / 4));
+  RT_DISPATCH(dtype, ej_of(n_experts), router_bwd_kernel, grid, s, (const T_*)logits, ld, n_tokens,
+              n_experts, idx, grad_w, top_k, softmax, norm, scale, (T_*)grad_logits_out, out_ld);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+extern "C" int moe_router_bias_update(float* bias, const int32_t* counts, int n_experts, float u,
+                                      void* stream) {
+  if (n_experts <= 0) return MOE_ERR_SHAPE;
+  if (!(u > 0.f)) return MOE_OK;  // u <= 0 (or NaN): no update, as the reference returns early
+  if (!bias || !counts) return MOE_ERR_SHAPE;
+  hipLaunchKernelGGL(router_bias_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, bias, counts,
+                     n_experts, u);
+  return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}

@@ -19,6 +19,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
 _S = ctypes.c_size_t
+_F = ctypes.c_float
 
 # name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
 _SIGS = {
@@ -42,6 +43,9 @@ _SIGS = {
     "moe_glu_bwd": [_I, _P, _L, _L, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P],
     "moe_fp8_fwd": [_P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P, _P, _P],
     "moe_rowquant_fp8": [_P, _L, _L, _P, _P, _P],
+    "moe_router_topk_fwd": [_I, _P, _L, _L, _I, _P, _I, _I, _I, _F, _P, _P, _P, _P],
+    "moe_router_topk_bwd": [_I, _P, _L, _L, _I, _P, _P, _I, _I, _I, _F, _P, _L, _P],
+    "moe_router_bias_update": [_P, _P, _I, _F, _P],
     "moe_mxfp8_fwd": [_P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P],
 }
 _RESTYPES = {"moe_version": ctypes.c_char_p, "moe_gate_grad_parts": ctypes.c_int, "moe_get_workspace_size": ctypes.c_size_t}
