@@ -168,6 +168,32 @@ def run_mxfp8(steps, warmup):
                          f"E={cfg['E']} k={k}, peak {PEAK_HBM_GBS} GB/s")}
 
 
+def run_router(steps, warmup):
+    """Router epilogue on config 3's routing shape: fp32 logits (N=16384, E=64),
+    sigmoid + selection bias + top-8 + norm + counts, then the backward from a random grad_w.
+    HBM-bound; algorithmic bytes: fwd N*E*4 read + N*k*12 written, bwd N*E*4 + N*k*12 read +
+    N*E*4 written."""
+    import torch
+    from kernels.gfx950.router import router_topk
+    n, e, k = 16384, 64, 8
+    g = torch.Generator(device="cuda").manual_seed(0)
+    logits = torch.randn(n, e, device="cuda", generator=g).requires_grad_(True)
+    bias = torch.randn(e, device="cuda", generator=g) * 0.01
+    gw = torch.randn(n, k, device="cuda", generator=g)
+
+    def step():
+        _, w, _ = router_topk(logits, bias, k, e)
+        w.backward(gw)
+    ms, kern = _timed(step, steps, warmup)
+    fwd, bwd = kern.get("moe_router_topk_fwd"), kern.get("moe_router_topk_bwd")
+    fb = n * e * 4 + n * k * 12
+    bb = n * e * 8 + n * k * 12
+    return {"fwd_us": round(fwd * 1e3, 2), "bwd_us": round(bwd * 1e3, 2),
+            "fwd_gbs": round(fb / (fwd * 1e-3) / 1e9, 1), "bwd_gbs": round(bb / (bwd * 1e-3) / 1e9, 1),
+            "frac_of_peak": round((fb + bb) / ((fwd + bwd) * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "workload": f"router epilogue fwd+bwd, fp32 logits N={n} E={e} top-{k}, sigmoid, bias, norm"}
+
+
 def cpu_baseline(config, sample_tokens, reps=3):
     """The oracle's fp32 eager MoE fwd+bwd (a restatement of the reference moe_eager, PyTorch on
     the host cores), on the first `sample_tokens` tokens of the same workload."""
@@ -270,6 +296,8 @@ def main():
         line["extra_configs"]["fp8_fwd"] = run_fp8(max(5, args.steps // 2), 2)
         _log("extra config 5 (MXFP8 decode)")
         line["extra_configs"]["mxfp8_decode"] = run_mxfp8(max(10, args.steps), 3)
+        _log("extra: router epilogue")
+        line["extra_configs"]["router_epilogue"] = run_router(max(10, args.steps), 3)
     if not args.no_cpu:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)

@@ -157,3 +157,15 @@ def test_router_counts_deterministic():
     a = router_topk(x, None, 8, 64)[2]
     b = router_topk(x, None, 8, 64)[2]
     assert torch.equal(a, b) and int(a.sum()) == 16384 * 8
+
+
+@pytest.mark.parametrize("e", [64, 200, 300])
+def test_router_exact_ties_pick_lower_expert(e):
+    _say(f"router ties E={e}")
+    g = torch.Generator().manual_seed(e)
+    logits = torch.randint(-3, 4, (500, e), generator=g).float()
+    idx, w, counts = router_topk(logits.cuda(), None, 8, e, False)
+    ridx, rw, rc = ro.router_topk(logits, None, 8, False)
+    assert torch.equal(idx.cpu(), ridx)
+    assert torch.equal(counts.cpu().long(), rc)
+    torch.testing.assert_close(w.cpu(), rw, rtol=1e-6, atol=1e-7)

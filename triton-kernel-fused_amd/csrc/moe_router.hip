@@ -9,6 +9,8 @@
 // (selection value, expert, score). Ties pick the lowest expert index. Counts are summed per
 // workgroup in LDS and added to the global counters with one integer atomic per expert, so the
 // totals do not depend on the order of the atomics.
+#include <algorithm>
+
 #include "moe_common.h"
 
 namespace moe {
@@ -16,6 +18,9 @@ namespace moe {
 constexpr int RT_THREADS = 256;  // 4 waves = 4 token rows per workgroup
 constexpr int RT_MAX_E = 1024;
 constexpr int RT_MAX_K = 32;
+constexpr int RT_RANK_E = 256;   // rank selection for E <= 256 (one LDS row per wave)
+constexpr int RT_MAX_GRID = 1 << 20;  // forward workgroups (grid-stride over rows beyond)
+constexpr int RT_COUNT_GRID = 64;    // count workgroups
 
 __device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -45,15 +50,20 @@ __device__ __forceinline__ float wave_add(float v) {
   return v;
 }
 
-// Scores of this lane's experts for one row (invalid experts: score 0).
+// This lane's logits of one row (invalid experts: -inf).
 template <typename T, int EJ>
-__device__ __forceinline__ void row_scores(const T* row, int E, int softmax, int lane, float (&s)[EJ]) {
-  float x[EJ];
+__device__ __forceinline__ void row_load(const T* row, int E, int lane, float (&x)[EJ]) {
 #pragma unroll
   for (int j = 0; j < EJ; ++j) {
     const int e = lane + 64 * j;
     x[j] = e < E ? to_f32(row[e]) : -INFINITY;
   }
+}
+
+// Scores of this lane's experts for one row from its logits (invalid experts: score 0).
+template <int EJ>
+__device__ __forceinline__ void row_scores_of(const float (&x)[EJ], int E, int softmax, int lane,
+                                              float (&s)[EJ]) {
   if (softmax) {
     float m = -INFINITY;
 #pragma unroll
@@ -79,23 +89,66 @@ template <typename T, int EJ>
 __global__ void __launch_bounds__(RT_THREADS)
 router_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
                   const float* __restrict__ bias, int top_k, int softmax, int norm, float scale,
-                  int64_t* __restrict__ idx_out, float* __restrict__ w_out,
-                  int32_t* __restrict__ counts) {
-  __shared__ int s_cnt[RT_MAX_E];
+                  int64_t* __restrict__ idx_out, float* __restrict__ w_out) {
+  __shared__ __attribute__((aligned(16))) float s_sel[(RT_THREADS / 64) * RT_RANK_E];
   const int lane = threadIdx.x & 63;
-  const int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
-  if (counts) {
-    for (int e = threadIdx.x; e < E; e += RT_THREADS) s_cnt[e] = 0;
-    __syncthreads();
-  }
-  if (n < N) {
-    float s[EJ], sel[EJ];
-    row_scores<T, EJ>(logits + n * ld, E, softmax, lane, s);
+  // Grid-stride over rows; the next row's logits are loaded while this row is processed.
+  const int64_t step = (int64_t)gridDim.x * (RT_THREADS / 64);
+  int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
+  float xn[EJ];
+  if (n < N) row_load<T, EJ>(logits + n * ld, E, lane, xn);
+  for (; n < N; n += step) {
+    float s[EJ], sel[EJ], x[EJ];
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) x[j] = xn[j];
+    if (n + step < N) row_load<T, EJ>(logits + (n + step) * ld, E, lane, xn);
+    row_scores_of<EJ>(x, E, softmax, lane, s);
 #pragma unroll
     for (int j = 0; j < EJ; ++j) {
       const int e = lane + 64 * j;
       sel[j] = e < E ? s[j] + (bias ? bias[e] : 0.f) : -INFINITY;
     }
+    if constexpr (EJ <= 4) {
+      // Rank selection: every lane counts, for each of its experts, the experts that beat it
+      // (larger value, or equal value and lower index) over the row's values in LDS; ranks below
+      // top_k are the picks, in order.
+      float* sb = s_sel + (threadIdx.x >> 6) * RT_RANK_E;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // previous row's reads are done
+#pragma unroll
+      for (int j = 0; j < EJ; ++j)
+        if (lane + 64 * j < E) sb[lane + 64 * j] = sel[j];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the row is in LDS for every lane
+      int rank[EJ];
+#pragma unroll
+      for (int j = 0; j < EJ; ++j) rank[j] = 0;
+#pragma unroll 4
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const f32x4 v = *(const f32x4*)(sb + e4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int eo = e4 + u;
+#pragma unroll
+          for (int j = 0; j < EJ; ++j) {
+            const int e = lane + 64 * j;
+            rank[j] += (eo < E) & ((v[u] > sel[j]) | ((v[u] == sel[j]) & (eo < e)));
+          }
+        }
+      }
+      float tsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < EJ; ++j)
+        if (lane + 64 * j < E && rank[j] < top_k) tsum += s[j];
+      tsum = wave_add(tsum);
+      const float f = norm ? scale / (tsum + 1e-20f) : scale;
+#pragma unroll
+      for (int j = 0; j < EJ; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && rank[j] < top_k) {
+          idx_out[n * top_k + rank[j]] = e;
+          w_out[n * top_k + rank[j]] = s[j] * f;
+        }
+      }
+    } else {
     // Lane k keeps pick k (every lane sees the same winner after the butterfly).
     float my_w = 0.f, tsum = 0.f;
     int my_e = 0;
@@ -125,14 +178,24 @@ router_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
     if (lane < top_k) {
       idx_out[n * top_k + lane] = my_e;
       w_out[n * top_k + lane] = my_w * f;
-      if (counts) atomicAdd(&s_cnt[my_e], 1);
+    }
     }
   }
-  if (counts) {
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += RT_THREADS)
-      if (s_cnt[e]) atomicAdd(&counts[e], s_cnt[e]);
-  }
+}
+
+// counts[e] += #{picks == e}: per-workgroup LDS histogram, then one global atomic per expert and
+// workgroup (a small grid keeps the atomics on each counter few).
+__global__ void __launch_bounds__(RT_THREADS)
+router_count_kernel(const int64_t* __restrict__ idx, int64_t n_picks, int E, int32_t* counts) {
+  __shared__ int s_cnt[RT_MAX_E];
+  for (int e = threadIdx.x; e < E; e += RT_THREADS) s_cnt[e] = 0;
+  __syncthreads();
+  for (int64_t i = (int64_t)blockIdx.x * RT_THREADS + threadIdx.x; i < n_picks;
+       i += (int64_t)gridDim.x * RT_THREADS)
+    atomicAdd(&s_cnt[(int)idx[i]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += RT_THREADS)
+    if (s_cnt[e]) atomicAdd(&counts[e], s_cnt[e]);
 }
 
 // grad_logits[n, e] from grad_w (fp32, (N, k)): with picked raw scores w_k and T = sum w_k + 1e-20,
@@ -148,7 +211,11 @@ router_bwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
   const int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
   if (n >= N) return;
   float s[EJ];
-  row_scores<T, EJ>(logits + n * ld, E, softmax, lane, s);
+  {
+    float x[EJ];
+    row_load<T, EJ>(logits + n * ld, E, lane, x);
+    row_scores_of<EJ>(x, E, softmax, lane, s);
+  }
   // Lane k (< top_k) holds slot k: its expert, upstream gradient and raw picked score.
   int ek = -1;
   float gk = 0.f, wk = 0.f;
@@ -255,9 +322,15 @@ extern "C" int moe_router_topk_fwd(int dtype, const void* logits, int64_t ld, in
   if (n_tokens == 0) return MOE_OK;
   if (!logits || !idx_out || !w_out) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)((n_tokens + 3) / 4));
-  RT_DISPATCH(dtype, ej_of(n_experts), router_fwd_kernel, grid, s, (const T_*)logits, ld, n_tokens,
-              n_experts, bias, top_k, softmax, norm, scale, idx_out, w_out, counts);
+  const dim3 fgrid((unsigned)std::min<int64_t>((n_tokens + 3) / 4, RT_MAX_GRID));
+  RT_DISPATCH(dtype, ej_of(n_experts), router_fwd_kernel, fgrid, s, (const T_*)logits, ld, n_tokens,
+              n_experts, bias, top_k, softmax, norm, scale, idx_out, w_out);
+  if (counts) {
+    const int64_t picks = n_tokens * top_k;
+    const unsigned cg = (unsigned)std::min<int64_t>((picks + RT_THREADS - 1) / RT_THREADS, RT_COUNT_GRID);
+    hipLaunchKernelGGL(router_count_kernel, dim3(cg), dim3(RT_THREADS), 0, s, idx_out, picks,
+                       n_experts, counts);
+  }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
