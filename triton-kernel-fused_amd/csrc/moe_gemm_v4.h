@@ -27,7 +27,8 @@ constexpr int NT = 512;
 constexpr int NW = NT / 64;
 constexpr int TILE = 256;
 constexpr int WP = 128;          // P rows (MFMA A side, output channels) per wave
-constexpr int WQ = 64;           // Q rows (MFMA B side, tokens) per wave
+constexpr int WQ = TILE / (NW / 2);  // Q rows (MFMA B side, tokens) per wave
+constexpr int RPW = TILE / NW;   // operand rows (Kc) or K rows x 4 (Rc) each wave loads per slot
 constexpr int TI = WP / 32;      // 4
 constexpr int TJ = WQ / 32;      // 2
 constexpr int OPB = TILE * ROWB; // 32 KB: one operand's K step
@@ -63,16 +64,22 @@ struct KcLoad {
     sw = (l >> 1) & 7;
   }
   __device__ __forceinline__ static int row_of(int i) {
-    return ((int)threadIdx.x >> 6) * 32 + i * 8 + (lane_id() >> 3);
+    return ((int)threadIdx.x >> 6) * RPW + i * 8 + (lane_id() >> 3);
   }
   __device__ __forceinline__ void prime(int) {}
   template <typename T>
   __device__ __forceinline__ void issue(char* slot, int k) {
-    char* base = slot + wave_id() * 32 * ROWB;
+    char* base = slot + wave_id() * RPW * ROWB;
     const int kb = k * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) dma16(rowp[i] + kb + cbyte[i & 1], base + i * 8 * ROWB);
   }
+  // One of the LOADS instructions of issue(), then issue_done() after the last.
+  template <typename T, int I>
+  __device__ __forceinline__ void issue_i(char* slot, int k) {
+    dma16(rowp[I] + k * (int)sizeof(T) + cbyte[I & 1], slot + wave_id() * RPW * ROWB + I * 8 * ROWB);
+  }
+  __device__ __forceinline__ void issue_done(int) {}
   template <int CPL>
   __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int c) const {
     const int cb = (((2 * sl + half) * CPL + c) ^ sw) << 4;
@@ -100,7 +107,7 @@ struct RcLoad {
   int cbyte[2];       // column byte offsets for even / odd i (clamped inside the operand)
   int zoff[2];        // zero-block offsets of the same chunks
   int toff[NFRAG];    // fragment reads: byte offset of fragment t for slab 0
-  int gi[8];          // GATHER: row indices of this wave's 8 K rows of the next issue
+  int gi[2 * LOADS];  // GATHER: row indices of this wave's K rows of the next issue
 
   // rbase: first column (r) of this wave's fragment block; rvalid: columns inside the operand.
   __device__ __forceinline__ void init(int rbase, int rvalid) {
@@ -119,27 +126,30 @@ struct RcLoad {
   }
   __device__ __forceinline__ void fetch_rows(int k) {
     if constexpr (GATHER) {
-      const int kw = k + wave_id() * 8;
+      const int kw = k + wave_id() * 2 * LOADS;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) gi[j] = v3::sload(gather + min(kw + j, kend - 1));
+      for (int j = 0; j < 2 * LOADS; ++j) gi[j] = v3::sload(gather + min(kw + j, kend - 1));
     }
   }
   // Called once with the first K of the operand's first issue.
   __device__ __forceinline__ void prime(int k) { fetch_rows(k); }
+  template <typename T, int I>
+  __device__ __forceinline__ void issue_i(char* slot, int k) {
+    const int w = wave_id(), h = lane_id() >> 5;
+    const int kk = k + w * 2 * LOADS + 2 * I;  // K row of lanes 0-31; lanes 32-63 take kk + 1
+    int row;
+    if constexpr (GATHER) row = h ? gi[2 * I + 1] : gi[2 * I];
+    else row = kk + h;
+    const char* g = (kk + h < kend) ? src + (size_t)row * ld + cbyte[I & 1]
+                                    : (const char*)v3::g_zero_block + zoff[I & 1];
+    dma16(g, slot + w * (2 * LOADS * RC_ROWB) + I * 1024);
+  }
+  // After the last issue_i of a slot: the gathered row indices of the next issue.
+  __device__ __forceinline__ void issue_done(int k) { fetch_rows(k + 64); }
   template <typename T>
   __device__ __forceinline__ void issue(char* slot, int k) {
-    const int w = wave_id(), h = lane_id() >> 5;
-    static_for<0, LOADS>([&](auto ic) {
-      constexpr int I = decltype(ic)::value;
-      const int kk = k + w * 8 + 2 * I;  // K row of lanes 0-31; lanes 32-63 take kk + 1
-      int row;
-      if constexpr (GATHER) row = h ? gi[2 * I + 1] : gi[2 * I];
-      else row = kk + h;
-      const char* g = (kk + h < kend) ? src + (size_t)row * ld + cbyte[I & 1]
-                                      : (const char*)v3::g_zero_block + zoff[I & 1];
-      dma16(g, slot + w * (8 * RC_ROWB) + I * 1024);
-    });
-    fetch_rows(k + 64);
+    static_for<0, LOADS>([&](auto ic) { issue_i<T, decltype(ic)::value>(slot, k); });
+    issue_done(k);
   }
   template <int CPL>
   __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int) const {
@@ -183,11 +193,14 @@ __device__ __forceinline__ void wait_slots(int n) {
 }
 
 // K loop over the ring: acc[ti][tj] += P(wave block) . Q(wave block) over K in [k0, k1). Step s
-// reads P_s from slot (2s) % NSLOT and Q_s from (2s+1) % NSLOT. The synchronisation sits before
-// the last slab of each step: wait for this wave's loads of step s+1, barrier, refill the two
-// slots step s has finished reading (with Q_{s+2} and P_{s+3}), read the first slab of step s+1,
-// then run the last slab's MFMAs, whose operands were read before the barrier and which cover the
-// latency of those reads.
+// reads P_s from slot (2s) % NSLOT and Q_s from (2s+1) % NSLOT. The synchronisation sits at the
+// last slab of each step and is the same at every step: wait for this wave's loads of step s+1
+// (one slot, P_{s+2}, may stay in flight), barrier, read the first slab of step s+1, then run the
+// last slab's MFMAs with the two refills of the slots step s has finished (Q_{s+2}, P_{s+3})
+// issued one DMA after each MFMA. Spreading the DMAs over the MFMAs and keeping the loop free of
+// branches measured ~5% faster than issuing them in a burst before the MFMAs. Refills past the
+// end re-read the last K step into slots nobody reads again, and the prologue always fills all
+// five slots the same way, so every wait is a constant; the loop end waits for all DMAs.
 template <typename T, class LP, class LQ>
 __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ& lq, int k0, int k1,
                                               char* smem) {
@@ -197,19 +210,18 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
   static_assert(SLABS >= 2, "the mid-step barrier needs at least two slabs per step");
   const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;
-  const int nslab = 2 * nk;  // ring loads of the whole loop: P_j is load 2j, Q_j is load 2j+1
 
   // Prologue: loads 0..NSLOT-1 (P0 Q0 P1 Q1 P2) into slots 0..4.
   lp.prime(k0);
   lq.prime(k0);
-  int issued = 0;
-  for (; issued < NSLOT && issued < nslab; ++issued) {
-    char* slot = smem + issued * SLOTB;
-    const int k = k0 + (issued >> 1) * KS;
-    if (issued & 1) lq.template issue<T>(slot, k);
+  const int klast = k0 + (nk - 1) * KS;
+  for (int i = 0; i < NSLOT; ++i) {
+    char* slot = smem + i * SLOTB;
+    const int k = min(k0 + (i >> 1) * KS, klast);
+    if (i & 1) lq.template issue<T>(slot, k);
     else lp.template issue<T>(slot, k);
   }
-  wait_slots(issued - 2);
+  wait_slots(NSLOT - 2);
   bare_barrier();
 
   // Operand fragments are double-buffered in registers (slab sl+1 read while slab sl's MFMAs run)
@@ -232,20 +244,6 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
   };
-  // Mid-step synchronisation: step s+1 landed (this wave's loads, then the barrier), and the two
-  // slots of step s are refilled with Q_{s+2} (slot sp) and P_{s+3} (slot sq).
-  auto sync_refill = [&](int s, int sp, int sq) {
-    wait_slots(issued - (2 * s + 4));
-    bare_barrier();
-    if (issued < nslab) {
-      lq.template issue<T>(smem + sp * SLOTB, k0 + (s + 2) * KS);
-      ++issued;
-    }
-    if (issued < nslab) {
-      lp.template issue<T>(smem + sq * SLOTB, k0 + (s + 3) * KS);
-      ++issued;
-    }
-  };
   int sp = 0, sq = 1;  // slots of P_s, Q_s
   if constexpr (FB == 2) load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
   for (int s = 0; s < nk; ++s) {
@@ -257,26 +255,70 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
     for (int sl = 0; sl < SLABS; ++sl) {
       if constexpr (FB == 2) {
         const int f = sl & 1;
-        if (sl + 1 < SLABS) {
-          load(f ^ 1, ps, qs, sl + 1);
-        } else if (s + 1 < nk) {
-          sync_refill(s, sp, sq);
+        if (sl + 1 == SLABS) {
+          // Synchronisation step, the same at every step (no branches around the MFMAs): wait for
+          // step s+1, barrier, read its first slab, and issue the two refills one DMA per MFMA of
+          // this slab. Past the last step the refills re-read the last K step into slots that are
+          // never read again, and the reads of "step s+1" read stale LDS into unused registers;
+          // the loop end drains the DMAs.
+          wait_slots(1);
+          bare_barrier();
           load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
+          const int kq = min(k0 + (s + 2) * KS, klast), kp = min(k0 + (s + 3) * KS, klast);
+          char* qslot = smem + sp * SLOTB;
+          char* pslot = smem + sq * SLOTB;
+          __builtin_amdgcn_sched_barrier(0);
+          static_assert(TI * TJ == 2 * LOADS, "one refill DMA per MFMA");
+          static_for<0, TI * TJ>([&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            Mfma<T>::step(acc[I / TJ][I % TJ], a[f][I / TJ][0], b[f][I % TJ][0]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (I < LOADS) lq.template issue_i<T, I>(qslot, kq);
+            else lp.template issue_i<T, I - LOADS>(pslot, kp);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+          lq.issue_done(kq);
+          lp.issue_done(kp);
+        } else {
+          load(f ^ 1, ps, qs, sl + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(f);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(f);
       } else {
         load(0, ps, qs, sl);
-        if (sl + 1 == SLABS && s + 1 < nk) sync_refill(s, sp, sq);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(0);
+        if (sl + 1 == SLABS) {
+          // As for 16-bit operands, with single-buffered fragments: the barrier also waits for
+          // this slab's fragment reads before the slots are refilled.
+          wait_slots(1);
+          bare_barrier();
+          const int kq = min(k0 + (s + 2) * KS, klast), kp = min(k0 + (s + 3) * KS, klast);
+          char* qslot = smem + sp * SLOTB;
+          char* pslot = smem + sq * SLOTB;
+          __builtin_amdgcn_sched_barrier(0);
+          static_assert(TI * TJ == 2 * LOADS, "one refill DMA per MFMA");
+          static_for<0, TI * TJ>([&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            Mfma<T>::stepf(acc[I / TJ][I % TJ], a[0][I / TJ], b[0][I % TJ]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (I < LOADS) lq.template issue_i<T, I>(qslot, kq);
+            else lp.template issue_i<T, I - LOADS>(pslot, kp);
+            __builtin_amdgcn_sched_barrier(0);
+          });
+          lq.issue_done(kq);
+          lp.issue_done(kp);
+        } else {
+          __builtin_amdgcn_sched_barrier(0);
+          mfmas(0);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     sp = np;
     sq = nq;
   }
-  // The epilogue reuses the LDS: every wave's reads of the last step must be over.
+  // The epilogue reuses the LDS: every wave's reads of the last step must be over (and, with the
+  // interleaved refills, every DMA into the ring has landed).
+  wait_slots(0);
   bare_barrier();
 }
 
