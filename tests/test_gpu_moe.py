@@ -222,3 +222,16 @@ def test_bf16_partial_grads_and_strided_grad_out(needs):
     key = {"wt": "grad_wt", "down": "grad_down", "gate_up": "grad_gate_up",
            "hidden": "grad_hidden"}[needs]
     _assert_bf16({key: d[needs].grad}, ref, keys=(key,))
+
+
+@pytest.mark.parametrize("h,i", [(64, 64), (128, 64), (64, 192), (192, 320)])
+def test_bf16_short_k_loops(h, i):
+    """One- to five-step K loops of the ring kernels (every K here is a multiple of 64): the
+    prologue and refills past the last step must not disturb the result."""
+    codes = [0, 1, 0, 1, 3]
+    hid, idx, w, gu, dw, codes_t, ap, go = _case(codes, 4, dtype=torch.bfloat16, n=300, h=h, i=i,
+                                                 k=2, seed=h + i)
+    _say(f"bf16 short K h={h} i={i}")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
+    mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
+    _assert_bf16(mine, ref)
