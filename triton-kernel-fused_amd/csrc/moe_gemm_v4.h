@@ -197,8 +197,8 @@ __device__ __forceinline__ void wait_slots(int n) {
 // last slab of each step and is the same at every step: wait for this wave's loads of step s+1
 // (one slot, P_{s+2}, may stay in flight), barrier, read the first slab of step s+1, then run the
 // last slab's MFMAs. The refills of the slots step s has finished go out between MFMAs: Q_{s+2}
-// one DMA after every second MFMA of that slab, P_{s+3} the same way during the first slab of step
-// s+1; every other slab interleaves the next slab's fragment reads with its MFMAs. Spreading the
+// one DMA after every second MFMA of that slab, P_{s+3} one DMA per four MFMAs over the first two
+// slabs of step s+1; every other slab interleaves the next slab's fragment reads with its MFMAs. Spreading the
 // DMAs and LDS reads over the MFMAs and keeping the loop free of branches measured ~8% faster
 // than issuing them in bursts. Refills past the end re-read the last K step into slots nobody
 // reads again, and the prologue fills the slots the same way at every K length, so every wait is
@@ -263,7 +263,7 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
         if (sl + 1 == SLABS) {
           // Synchronisation step, the same at every step (no branches around the MFMAs): wait for
           // step s+1, barrier, read its first slab, and issue the Q refill one DMA per two MFMAs;
-          // the P refill goes out the same way during the next step's first slab. Past the last
+          // the P refill goes out over the next step's first two slabs. Past the last
           // step the refills re-read the last K step into slots that are never read again, and
           // the reads of "step s+1" read stale LDS into unused registers; the loop end drains the
           // DMAs.
@@ -285,7 +285,8 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
           pp_slot = sq;
           pp_k = kp;
         } else {
-          // Next slab's fragment reads (and, in slab 0, the pending P refill) between the MFMAs.
+          // Next slab's fragment reads (and, in slabs 0 and 1, the pending P refill) between the
+          // MFMAs.
           static_for<0, TI * TJ>([&](auto ic) {
             constexpr int I = decltype(ic)::value;
             if constexpr (I < TI) a[f ^ 1][I][0] = lp.template frag<CPL>(ps, I, sl + 1, 0);
@@ -293,12 +294,13 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
             __builtin_amdgcn_sched_barrier(0);
             Mfma<T>::step(acc[I / TJ][I % TJ], a[f][I / TJ][0], b[f][I % TJ][0]);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (I % 2 == 1) {
-              if (sl == 0) lp.template issue_i<T, I / 2>(smem + pp_slot * SLOTB, pp_k);
+            if constexpr (I % 4 == 3) {
+              if (sl == 0) lp.template issue_i<T, I / 4>(smem + pp_slot * SLOTB, pp_k);
+              if (sl == 1) lp.template issue_i<T, 2 + I / 4>(smem + pp_slot * SLOTB, pp_k);
             }
             __builtin_amdgcn_sched_barrier(0);
           });
-          if (sl == 0) lp.issue_done(pp_k);
+          if (sl == 1) lp.issue_done(pp_k);
         }
       } else {
         load(0, ps, qs, sl);
