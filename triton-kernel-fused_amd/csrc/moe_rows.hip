@@ -83,9 +83,9 @@ __device__ __forceinline__ int slot_kind(int64_t e, const int32_t* codes, int E_
   return c == 3 ? 1 : 2;
 }
 
-// Per-token gathers (combine forward, un-permute backward). One wave owns cpw consecutive
-// 64*V-column chunks of one token; for each chunk the k routed rows are loaded BATCH at a time
-// (the token's routing reads are wave-uniform) and summed in slot order in fp32:
+// Per-token gathers (combine forward, un-permute backward). One wave owns one 64*V-column chunk
+// of one token; the k routed rows are loaded BATCH at a time, all BATCH loads in flight together
+// (the token's routing reads are wave-uniform), and summed in slot order in fp32:
 //   acc = sum_j g_j * row_j,  row_j = rows[f2s[t,j]] for a GLU expert (g_j = gate if GATE_GLU,
 //   else 1) or self[t] for an Identity expert (g_j = gate); Zero experts and invalid ids add
 //   nothing.
@@ -95,49 +95,47 @@ __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T
                                              const int64_t* __restrict__ idx,
                                              const int32_t* __restrict__ codes, int E_glu,
                                              int E_all, const int32_t* __restrict__ f2s,
-                                             int64_t N, int k, int H, T* __restrict__ out,
-                                             int cpw) {
+                                             int64_t N, int k, int H, T* __restrict__ out) {
   constexpr int V = Vec8<T>::N;
   const int nchunk = (H + 64 * V - 1) / (64 * V);
-  const int ngroup = (nchunk + cpw - 1) / cpw;  // waves per token
   const int64_t wv = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
-  if (wv >= N * ngroup) return;
-  const int64_t t = wv / ngroup;
+  if (wv >= N * nchunk) return;
+  const int64_t t = wv / nchunk;
   const int lane = threadIdx.x & 63;
-  const int cg = (int)(wv % ngroup) * cpw;
-  for (int ci = cg; ci < cg + cpw && ci < nchunk; ++ci) {
-    const int c = ci * 64 * V + lane * V;
+  {
+    const int c = (int)(wv % nchunk) * 64 * V + lane * V;
     const bool col_ok = c < H;
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
     for (int j0 = 0; j0 < k; j0 += BATCH) {
-      float v[BATCH][V], w[BATCH];
+      // Branch-free: every slot's 16 bytes are loaded (a skipped slot reads the token's own row)
+      // before any is used, so the BATCH loads are in flight together.
+      const T* src[BATCH];
+      float w[BATCH];
+      bool used[BATCH];
 #pragma unroll
       for (int jj = 0; jj < BATCH; ++jj) {
         const int j = j0 + jj;
-        bool used = false;
-        if (j < k) {
-          const int64_t f = t * k + j;
-          const int pos = f2s[f];
-          const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
-          if (kind != 2 && col_ok) {
-            used = true;
-            w[jj] = (kind == 0 && !GATE_GLU) ? 1.f : to_f32(wt[f]);
-            if (kind == 0) Vec8<T>::ld(rows + (size_t)pos * H + c, v[jj]);
-            else Vec8<T>::ld(self + (size_t)t * self_ld + c, v[jj]);
-          }
-        }
-        if (!used) {  // skipped slot: contributes nothing (not even 0 * inf)
-          w[jj] = 0.f;
-#pragma unroll
-          for (int i = 0; i < V; ++i) v[jj][i] = 0.f;
-        }
+        const int64_t f = t * k + (j < k ? j : 0);
+        const int pos = f2s[f];
+        const int kind = j < k ? slot_kind(idx[f], codes, E_glu, E_all, pos) : 2;
+        used[jj] = kind != 2 && col_ok;
+        w[jj] = (kind == 0 && !GATE_GLU) ? 1.f : to_f32(wt[f]);
+        src[jj] = kind == 0 ? rows + (size_t)pos * H : self + (size_t)t * self_ld;
       }
+      i32x4 raw[BATCH];
+      const int cc = col_ok ? c : 0;
 #pragma unroll
-      for (int jj = 0; jj < BATCH; ++jj)
+      for (int jj = 0; jj < BATCH; ++jj) raw[jj] = *(const i32x4*)(src[jj] + cc);
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] += w[jj] * v[jj][i];
+      for (int jj = 0; jj < BATCH; ++jj) {
+        float v[V];
+        Vec8<T>::ld((const T*)&raw[jj], v);
+        // A skipped slot contributes nothing (not even 0 * inf).
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += used[jj] ? w[jj] * v[i] : 0.f;
+      }
     }
     if (col_ok) Vec8<T>::st(out + (size_t)t * H + c, acc);
   }
@@ -149,9 +147,8 @@ __global__ void __launch_bounds__(ROW_THREADS)
 combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
                    const T* __restrict__ wt, const int64_t* __restrict__ idx,
                    const int32_t* __restrict__ codes, int E_glu, int E_all,
-                   const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out,
-                   int cpw) {
-  token_gather<T, true, BATCH>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out, cpw);
+                   const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out) {
+  token_gather<T, true, BATCH>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out);
 }
 
 // Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
@@ -236,9 +233,9 @@ unpermute_bwd_kernel(const T* __restrict__ gxs, const T* __restrict__ go, int64_
                      const T* __restrict__ wt, const int64_t* __restrict__ idx,
                      const int32_t* __restrict__ codes, int E_glu, int E_all,
                      const int32_t* __restrict__ f2s, int64_t N, int k, int H,
-                     T* __restrict__ gx, int cpw) {
+                     T* __restrict__ gx) {
   // GLU expert rows of grad_xs already carry the gate weight; Identity slots add w * grad_out.
-  token_gather<T, false, BATCH>(gxs, go, go_ld, wt, idx, codes, E_glu, E_all, f2s, N, k, H, gx, cpw);
+  token_gather<T, false, BATCH>(gxs, go, go_ld, wt, idx, codes, E_glu, E_all, f2s, N, k, H, gx);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -418,18 +415,10 @@ static int check_rows(int dtype, int64_t n, int top_k, int64_t H, int n_experts,
 
 static unsigned row_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
 
-// Waves per token for the per-token gathers (combine, un-permute) and the 64*vec-column chunks
-// each wave sums (*cpw): one chunk per wave while that leaves fewer than ~16K waves (decode
-// batches; the rows are then loaded 8 at a time for memory-level parallelism), else whole-token
-// waves loading one row at a time (measured faster when the grid alone fills the GPU).
-static int64_t token_col_waves(int64_t n_tokens, int64_t H, int vec, int* cpw) {
-  const int64_t nchunk = (H + 64 * vec - 1) / (64 * vec);
-  const int64_t target = 16384;
-  int64_t c = n_tokens >= target ? nchunk : (n_tokens * nchunk + target - 1) / target;
-  c = c < 1 ? 1 : (c > nchunk ? nchunk : c);
-  *cpw = (int)c;
-  return (nchunk + c - 1) / c;
-}
+// Waves per token for the per-token gathers (combine, un-permute): one per 64*vec-column chunk.
+// Each wave keeps its token's 8 row loads in flight together; whole-token waves loading one row
+// at a time measured ~20% slower even when the grid alone fills the GPU.
+static int64_t token_col_waves(int64_t H, int vec) { return (H + 64 * vec - 1) / (64 * vec); }
 
 extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
                                const void* top_k_weights, const int64_t* top_k_indices,
@@ -443,19 +432,13 @@ extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
       (E_glu > 0 && !eo))
     return MOE_ERR_SHAPE;
   if (!al16(hidden) || !al16(out) || (eo && !al16(eo))) return MOE_ERR_ALIGN;
-  int cpw;
-  const int64_t col_waves = token_col_waves(n_tokens, H, vec_of(dtype), &cpw);
+  const int64_t col_waves = token_col_waves(H, vec_of(dtype));
   if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(row_grid(n_tokens * col_waves));
-  if (col_waves == 1)
-    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 1, grid, dim3(ROW_THREADS), s,
-                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out, cpw);
-  else
-    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 8, grid, dim3(ROW_THREADS), s,
-                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out, cpw);
+  MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 8, grid, dim3(ROW_THREADS), s,
+                 (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+                 act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -520,20 +503,13 @@ extern "C" int moe_unpermute_bwd(int dtype, const void* grad_xs, const void* gra
   if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
   if (!al16(grad_out) || !al16(grad_x_out) || (grad_xs && !al16(grad_xs))) return MOE_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  int cpw;
-  const int64_t col_waves = token_col_waves(n_tokens, H, vec_of(dtype), &cpw);
+  const int64_t col_waves = token_col_waves(H, vec_of(dtype));
   if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
   const dim3 grid(row_grid(n_tokens * col_waves));
-  if (col_waves == 1)
-    MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 1, grid, dim3(ROW_THREADS), s,
-                   (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
-                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
-                   (int)H, (T_*)grad_x_out, cpw);
-  else
-    MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 8, grid, dim3(ROW_THREADS), s,
-                   (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
-                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
-                   (int)H, (T_*)grad_x_out, cpw);
+  MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 8, grid, dim3(ROW_THREADS), s,
+                 (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
+                 top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+                 (int)H, (T_*)grad_x_out);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
