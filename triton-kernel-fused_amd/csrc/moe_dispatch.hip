@@ -16,9 +16,35 @@
 namespace moe {
 
 constexpr int DISPATCH_THREADS = 256;
-constexpr int DISPATCH_CHUNK = 4096;  // flat rows per chunk (16 steps of 256)
+constexpr int DISPATCH_CHUNK = 1024;  // flat rows per chunk (4 steps of 256)
 constexpr int MAX_EXPERTS = 1024;
 constexpr int TILE_ROWS = 128;        // token-tile height of the grouped GEMMs
+
+// Exclusive prefix sums over the block of up to NT * 2 values, two consecutive values per thread
+// (v0 at index 2t, v1 at 2t+1): p0/p1 get the sums of everything before them, the return value is
+// the total. s_w holds NT / 64 partial sums.
+template <int NT>
+__device__ __forceinline__ int block_scan2(int v0, int v1, int& p0, int& p1, int* s_w) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v0 + v1;  // inclusive scan of the pair sums over the wave
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) s_w[w] = x;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) {
+    const int s = s_w[i];
+    before += i < w ? s : 0;
+    total += s;
+  }
+  p0 = before + x - v0 - v1;
+  p1 = p0 + v0;
+  return total;
+}
 
 __device__ __forceinline__ int load_expert(const int64_t* idx, int64_t f, int E, bool& valid) {
   int64_t v = idx[f];
@@ -58,11 +84,17 @@ dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E, int32_t* __
   __shared__ int s_tiles[MAX_EXPERTS];
   const int e = threadIdx.x;
   if (e < E) {
+    // Eight chunks' counts are loaded before any is rewritten, so the loads overlap.
     int run = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      int v = hist[(int64_t)c * E + e];
-      hist[(int64_t)c * E + e] = run;
-      run += v;
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+      int v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = c0 + j < nchunks ? hist[(int64_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (c0 + j < nchunks) hist[(int64_t)(c0 + j) * E + e] = run;
+        run += v[j];
+      }
     }
     counts[e] = run;
     s_cnt[e] = run;
@@ -168,6 +200,7 @@ dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int
   __shared__ int run[MAX_EXPERTS + 1];
   __shared__ int wcnt[NW][MAX_EXPERTS + 1];
   __shared__ int s_bad;
+  __shared__ int s_scan[NW];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int e = tid; e <= E; e += SMALL_THREADS) cnt[e] = 0;
   if (tid == 0) s_bad = 0;
@@ -181,18 +214,23 @@ dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int
   }
   if (bad) atomicAdd(&s_bad, bad);
   __syncthreads();
-  if (tid == 0) {
-    int o = 0, tt = 0;
-    for (int i = 0; i < E; ++i) {
-      offsets[i] = o;
-      tile_offsets[i] = tt;
-      run[i] = o;
-      o += cnt[i];
-      tt += (cnt[i] + TILE_ROWS - 1) / TILE_ROWS;
+  {
+    // Offsets and tile offsets: block-wide exclusive scans (experts 2*tid and 2*tid + 1).
+    static_assert(2 * SMALL_THREADS >= MAX_EXPERTS, "two experts per thread");
+    const int e0 = 2 * tid, e1 = 2 * tid + 1;
+    const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
+    int o0, o1, t0, t1;
+    const int o_tot = block_scan2<SMALL_THREADS>(c0, c1, o0, o1, s_scan);
+    __syncthreads();  // s_scan is reused
+    const int t_tot = block_scan2<SMALL_THREADS>((c0 + TILE_ROWS - 1) / TILE_ROWS,
+                                                 (c1 + TILE_ROWS - 1) / TILE_ROWS, t0, t1, s_scan);
+    if (e0 < E) { offsets[e0] = o0; tile_offsets[e0] = t0; run[e0] = o0; }
+    if (e1 < E) { offsets[e1] = o1; tile_offsets[e1] = t1; run[e1] = o1; }
+    if (tid == 0) {
+      offsets[E] = o_tot;
+      tile_offsets[E] = t_tot;
+      if (s_bad) atomicAdd(status, s_bad);
     }
-    offsets[E] = o;
-    tile_offsets[E] = tt;
-    if (s_bad) atomicAdd(status, s_bad);
   }
   // Experts by descending count (ties by id).
   for (int e = tid; e < E; e += SMALL_THREADS) {
