@@ -44,7 +44,8 @@ def test_dispatch_baseline_routing(config):
 
 @pytest.mark.parametrize("n,k,e,seed", [(1, 1, 1, 0), (4096, 1, 3, 1), (4097, 1, 3, 2),
                                         (2048, 2, 2, 3), (1000, 8, 1024, 4), (33333, 4, 257, 5),
-                                        (5, 3, 7, 6)])
+                                        (5, 3, 7, 6), (1024, 1, 5, 8), (1025, 1, 5, 9),
+                                        (128, 8, 256, 10), (129, 8, 256, 11), (511, 2, 1000, 12)])
 def test_dispatch_random(n, k, e, seed):
     g = torch.Generator().manual_seed(seed)
     idx = torch.rand(n, max(e, k), generator=g).topk(k, dim=-1).indices % e
