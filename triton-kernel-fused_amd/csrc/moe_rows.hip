@@ -194,7 +194,7 @@ combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict_
 // GLU expert: grad_wt[f] = sum of the n_parts partial dots of its sorted row (fixed order, so the
 // result is deterministic); Identity: <grad_out[t], hidden[t]>; Zero or invalid: 0
 // (kernels/sm75/moe.py:712-720).
-template <typename T>
+template <typename T, bool LANES>
 __global__ void __launch_bounds__(ROW_THREADS)
 gate_grad_kernel(const float* __restrict__ part, int n_parts, int64_t n_rows,
                  const T* __restrict__ go, int64_t go_ld, const T* __restrict__ hidden,
@@ -205,10 +205,27 @@ gate_grad_kernel(const float* __restrict__ part, int n_parts, int64_t n_rows,
   const int64_t t = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
   if (t >= N) return;
   const int lane = threadIdx.x & 63;
+  if (LANES) {
+    // k * n_parts <= 64, n_parts a power of two: lane = j * n_parts + p loads partial p of slot
+    // j, all in flight together, and each slot's n_parts lanes sum them (butterfly within the
+    // segment, a fixed order). Identity slots are handled by the loop below.
+    float v = 0.f;
+    int kind = 2;
+    const int j = lane / n_parts, p = lane & (n_parts - 1);
+    const int64_t f = t * k + (j < k ? j : 0);
+    if (j < k) {
+      const int pos = f2s[f];
+      kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+      if (kind == 0) v = part[(size_t)p * n_rows + pos];
+    }
+    for (int d = 1; d < n_parts; d <<= 1) v += __shfl_xor(v, d, 64);
+    if (j < k && p == 0 && kind != 1) grad_wt[f] = from_f32<T>(v);
+  }
   for (int j = 0; j < k; ++j) {
     const int64_t f = t * k + j;
     const int pos = f2s[f];
     const int kind = slot_kind(idx[f], codes, E_glu, E_all, pos);
+    if (LANES && kind != 1) continue;
     float v = 0.f;
     if (kind == 0) {
       for (int p = lane; p < n_parts; p += 64) v += part[(size_t)p * n_rows + pos];
@@ -481,10 +498,17 @@ extern "C" int moe_gate_grad(int dtype, const float* wt_partial, int n_parts, in
   if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
   if (!al16(grad_out) || !al16(hidden)) return MOE_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  MOE_BY_DTYPE(dtype, gate_grad_kernel, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
-               wt_partial, n_parts, n_rows, (const T_*)grad_out, grad_out_ld, (const T_*)hidden,
-               top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H,
-               (T_*)grad_wt_out);
+  const bool lanes = n_parts > 0 && (n_parts & (n_parts - 1)) == 0 && (int64_t)top_k * n_parts <= 64;
+  if (lanes)
+    MOE_BY_DTYPE_B(dtype, gate_grad_kernel, true, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
+                   wt_partial, n_parts, n_rows, (const T_*)grad_out, grad_out_ld, (const T_*)hidden,
+                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+                   (int)H, (T_*)grad_wt_out);
+  else
+    MOE_BY_DTYPE_B(dtype, gate_grad_kernel, false, dim3(row_grid(n_tokens)), dim3(ROW_THREADS), s,
+                   wt_partial, n_parts, n_rows, (const T_*)grad_out, grad_out_ld, (const T_*)hidden,
+                   top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
+                   (int)H, (T_*)grad_wt_out);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
