@@ -203,6 +203,9 @@ __device__ __forceinline__ void wait_slots(int n) {
 // than issuing them in bursts. Refills past the end re-read the last K step into slots nobody
 // reads again, and the prologue fills the slots the same way at every K length, so every wait is
 // a constant; the loop end waits for all DMAs.
+#ifndef V4_FP8_ROLL
+#define V4_FP8_ROLL 1
+#endif
 template <typename T, class LP, class LQ>
 __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ& lq, int k0, int k1,
                                               char* smem) {
@@ -249,8 +252,22 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
   };
+  // fp8 rolled fragments (V4_FP8_ROLL): one A buffer, two B buffers.
+  i32x4 ra[TI][CPL], rb[2][TJ][CPL];
   int sp = 0, sq = 1;  // slots of P_s, Q_s
   if constexpr (FB == 2) load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
+  if constexpr (FB == 1 && V4_FP8_ROLL) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+      for (int t = 0; t < TI; ++t) ra[t][c] = lp.template frag<CPL>(smem, t, 0, c);
+#pragma unroll
+      for (int t = 0; t < TJ; ++t) rb[0][t][c] = lq.template frag<CPL>(smem + SLOTB, t, 0, c);
+    }
+    // lgkmcnt(0) (vmcnt and expcnt at their maxima) as a real waitcnt instruction, so the
+    // compiler's loop-entry state holds no LDS reads and the in-loop waits stay partial.
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+  }
   for (int s = 0; s < nk; ++s) {
     const char* ps = smem + sp * SLOTB;
     const char* qs = smem + sq * SLOTB;
@@ -301,6 +318,51 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
             __builtin_amdgcn_sched_barrier(0);
           });
           if (sl == 1) lp.issue_done(pp_k);
+        }
+      } else if constexpr (V4_FP8_ROLL) {
+        // fp8: B fragments double-buffered (the next slab's reads after the slab's first MFMAs), A fragments
+        // rolled: each is re-read for the next slab right after its last MFMA of this slab, so
+        // every read has the rest of the slab's MFMAs to land, within the register budget of one
+        // buffer. The synchronising slab waits, barriers, then reads step s+1's first slab the
+        // same way and issues the refills one DMA per MFMA.
+        const int f = sl & 1;
+        const bool sync = sl + 1 == SLABS;
+        const char* nps = sync ? smem + np * SLOTB : ps;
+        const char* nqs = sync ? smem + nq * SLOTB : qs;
+        const int nsl = sync ? 0 : sl + 1;
+        int kq = 0, kp = 0;
+        char* qslot = smem + sp * SLOTB;
+        char* pslot = smem + sq * SLOTB;
+        if (sync) {
+          wait_slots(1);
+          bare_barrier();
+          kq = min(k0 + (s + 2) * KS, klast);
+          kp = min(k0 + (s + 3) * KS, klast);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, TI * TJ>([&](auto ic) {
+          constexpr int I = decltype(ic)::value;
+          Mfma<T>::stepf(acc[I / TJ][I % TJ], ra[I / TJ], rb[f][I % TJ]);
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (I < TJ) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) rb[f ^ 1][I][c] = lq.template frag<CPL>(nqs, I, nsl, c);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (I % TJ == TJ - 1) {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) ra[I / TJ][c] = lp.template frag<CPL>(nps, I / TJ, nsl, c);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (sync) {
+            if constexpr (I < LOADS) lq.template issue_i<T, I>(qslot, kq);
+            else lp.template issue_i<T, I - LOADS>(pslot, kp);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        if (sync) {
+          lq.issue_done(kq);
+          lp.issue_done(kp);
         }
       } else {
         load(0, ps, qs, sl);
