@@ -55,6 +55,14 @@ template <> struct Mfma<bf16> {
   __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
     step(c, a[0], b[0]);
   }
+  // 16x16x32: lane l holds row (A) / column (B) l%16, K values 8(l/16) .. 8(l/16)+7.
+  __device__ __forceinline__ static void step(f32x4& c, i32x4 a, i32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void stepf(f32x4& c, const i32x4* a, const i32x4* b) {
+    step(c, a[0], b[0]);
+  }
 };
 
 template <> struct Mfma<f16> {
@@ -65,6 +73,13 @@ template <> struct Mfma<f16> {
                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
   __device__ __forceinline__ static void stepf(f32x16& c, const i32x4* a, const i32x4* b) {
+    step(c, a[0], b[0]);
+  }
+  __device__ __forceinline__ static void step(f32x4& c, i32x4 a, i32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                               __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void stepf(f32x4& c, const i32x4* a, const i32x4* b) {
     step(c, a[0], b[0]);
   }
 };

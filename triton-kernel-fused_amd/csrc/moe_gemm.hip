@@ -427,17 +427,15 @@ template <typename T> using V2Cfg = Cfg<T, v2::TILE, v2::TILE, 2, 2>;
 //   EPI_STORE   chunk c -> out channel rt*256 + wr*128 + 8c
 //   EPI_GLU_FWD chunk c < 8 -> gate channel rt*128 + wr*64 + 8c, chunk c + 8 -> the same up channel
 //   EPI_GLU_BWD chunk c -> grad_inter channel rt*256 + wr*128 + 8c
-// TJ = 32-row token tiles per wave (WQ = 32 TJ token rows); the wave holds channels wr*128..+127
+// WQ = token rows per wave; the wave holds channels wr*128..+127
 // of the 256-channel tile and token rows wc*WQ..+WQ-1.
-template <typename T, int EPI, int TJ = v2::TN>
-__device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ], const TokenArgs& a,
-                                                  int e, int m0, int m_end, int rt, char* smem,
-                                                  int wr, int wc) {
-  constexpr int WQ = 32 * TJ;
+template <typename T, int EPI, int WQ = 32 * v2::TN, class Acc>
+__device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArgs& a, int e, int m0,
+                                                  int m_end, int rt, char* smem, int wr, int wc) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   char* wl = smem + w * (WQ * v2::EPI_ROWB);
   const int row0 = m0 + wc * WQ;
-  v2::stage_acc<T, TJ>(acc, wl);
+  v2::stage_acc<T>(acc, wl);
   __syncthreads();
   if constexpr (EPI == EPI_STORE) {
     v2::store_staged<T, WQ>(wl, (T*)a.out, a.out_ld, row0, m_end, rt * v2::TILE + wr * v2::WT, a.R);
@@ -579,18 +577,38 @@ __device__ __forceinline__ void token_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ
 }
 
 // Weight-gradient epilogue of the 256x256 kernel: out[e, c, r], c = MFMA column, r contiguous.
-// TJ = 32-column tiles per wave (WQ = 32 TJ output rows c); the wave holds r = wr*128..+127.
-template <typename T, int TJ = v2::TN>
-__device__ __forceinline__ void wgrad_epilogue_v2(const f32x16 (&acc)[v2::TN][TJ], const WgradArgs& a,
-                                                  int e, int r0, int c0, char* smem, int wr, int wc) {
-  constexpr int WQ = 32 * TJ;
+// WQ = output rows c per wave; the wave holds r = wr*128..+127.
+template <typename T, int WQ = 32 * v2::TN, class Acc>
+__device__ __forceinline__ void wgrad_epilogue_v2(const Acc& acc, const WgradArgs& a, int e, int r0,
+                                                  int c0, char* smem, int wr, int wc) {
   const int w = threadIdx.x >> 6;
   char* wl = smem + w * (WQ * v2::EPI_ROWB);
-  v2::stage_acc<T, TJ>(acc, wl);
+  v2::stage_acc<T>(acc, wl);
   __syncthreads();
   v2::store_staged<T, WQ>(wl, (T*)a.out + (size_t)e * a.C * a.R, a.R, c0 + wc * WQ, a.C,
                           r0 + wr * v2::WT, a.R);
 }
+
+// MFMA tile shape of the 16-bit ring kernels: 16x16x32 (8 x 4 tiles of f32x4 per wave) or
+// 32x32x16 (4 x 2 tiles of f32x16). Measured on the config-3 GEMMs, the token GEMMs run 3-6%
+// faster on 16x16x32 tiles (same LDS and operand traffic, half the accumulator register traffic
+// per FLOP), the weight gradients (both operands read transposed) 3-7% slower.
+template <class AccV, int TI_, int TJ_, int FR_, class Kc_>
+struct V4Shape {
+  using Acc = AccV;
+  using Kc = Kc_;
+  static constexpr int TI = TI_, TJ = TJ_, FR = FR_;
+  __device__ __forceinline__ static void zero(Acc (&acc)[TI][TJ]) {
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj)
+#pragma unroll
+        for (int v = 0; v < (int)(sizeof(Acc) / sizeof(float)); ++v) acc[ti][tj][v] = 0.f;
+  }
+};
+using V4Sh16 = V4Shape<f32x4, v4::TI16, v4::TJ16, 16, v4::KcLoad16>;
+using V4Sh32 = V4Shape<f32x16, v4::TI, v4::TJ, 32, v4::KcLoad>;
 
 // Token GEMMs on the eight-wave ring kernel of moe_gemm_v4.h. The token side Q is K-contiguous
 // (gathered or sorted rows); the weights P are K-contiguous in the forward and row-contiguous
@@ -620,7 +638,7 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
   const int wr = v4::wave_r(), wc = v4::wave_c();
 
   // Token rows past the group end read row m0 (their results are never stored).
-  v4::KcLoad lq;
+  typename V4Sh16::Kc lq;
   lq.init(wc * v4::WQ);
 #pragma unroll
   for (int i = 0; i < v4::LOADS; ++i) {
@@ -630,16 +648,11 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
     lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
   }
 
-  f32x16 acc[v4::TI][v4::TJ];
-#pragma unroll
-  for (int ti = 0; ti < v4::TI; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < v4::TJ; ++tj)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  typename V4Sh16::Acc acc[V4Sh16::TI][V4Sh16::TJ];
+  V4Sh16::zero(acc);
 
   if constexpr (P_RC) {
-    v4::RcLoad<false, v4::TI> lp;
+    v4::RcLoad<false, V4Sh16::TI, V4Sh16::FR> lp;
     const int r0 = rt * v4::TILE;
     lp.src = (const char*)(Pe + r0);
     lp.ld = (size_t)a.p_ld * sizeof(T);
@@ -649,7 +662,7 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
     __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
     v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
   } else {
-    v4::KcLoad lp;
+    typename V4Sh16::Kc lp;
     lp.init(wr * v4::WP);
 #pragma unroll
     for (int i = 0; i < v4::LOADS; ++i) {
@@ -667,7 +680,7 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
     __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
     v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
   }
-  token_epilogue_v2<T, EPI, v4::TJ>(acc, a, e, m0, m_end, rt, smem, wr, wc);
+  token_epilogue_v2<T, EPI, v4::WQ>(acc, a, e, m0, m_end, rt, smem, wr, wc);
 }
 
 // Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
@@ -701,28 +714,23 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
   const int r0 = rt * v4::TILE, c0 = ct * v4::TILE;
   const int wr = v4::wave_r(), wc = v4::wave_c();
 
-  v4::RcLoad<RG, v4::TI> lp;
+  v4::RcLoad<RG, V4Sh32::TI, V4Sh32::FR> lp;
   lp.src = (const char*)((const T*)a.rsrc + r0);
   lp.ld = (size_t)a.r_ld * sizeof(T);
   lp.gather = a.r_gather;
   lp.kend = k1;
   lp.init(wr * v4::WP, a.R - r0);
-  v4::RcLoad<CG, v4::TJ> lq;
+  v4::RcLoad<CG, V4Sh32::TJ, V4Sh32::FR> lq;
   lq.src = (const char*)((const T*)a.csrc + c0);
   lq.ld = (size_t)a.c_ld * sizeof(T);
   lq.gather = a.c_gather;
   lq.kend = k1;
   lq.init(wc * v4::WQ, a.C - c0);
 
-  f32x16 acc[v4::TI][v4::TJ];
-#pragma unroll
-  for (int ti = 0; ti < v4::TI; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < v4::TJ; ++tj)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+  typename V4Sh32::Acc acc[V4Sh32::TI][V4Sh32::TJ];
+  V4Sh32::zero(acc);
   v4::mainloop_ring<T>(acc, lp, lq, k0, k1, smem);
-  wgrad_epilogue_v2<T, v4::TJ>(acc, a, e, r0, c0, smem, wr, wc);
+  wgrad_epilogue_v2<T, v4::WQ>(acc, a, e, r0, c0, smem, wr, wc);
 }
 
 // dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.

@@ -273,6 +273,23 @@ __device__ __forceinline__ void stage_acc(const f32x16 (&acc)[TN][TJ], char* wl)
   }
 }
 
+// The same for 16x16 MFMA tiles (acc[ti][tj]: lane l holds channels ti*16 + 4(l/16) + v, v < 4,
+// of output row tj*16 + l%16): chunk 2ti + l/32, half (l/16) & 1. A 32-lane half writes each of
+// its 16 rows' chunk once, all 64 banks.
+template <typename T, int TI_, int TJ_>
+__device__ __forceinline__ void stage_acc(const f32x4 (&acc)[TI_][TJ_], char* wl) {
+  const int lane = threadIdx.x & 63, h = (lane >> 4) & 1, g = lane >> 5;
+#pragma unroll
+  for (int tj = 0; tj < TJ_; ++tj) {
+    const int q = tj * 16 + (lane & 15);
+#pragma unroll
+    for (int ti = 0; ti < TI_; ++ti) {
+      uint2 v = {pack2<T>(acc[ti][tj][0], acc[ti][tj][1]), pack2<T>(acc[ti][tj][2], acc[ti][tj][3])};
+      *(uint2*)(wl + staged_off(q, 2 * ti + g) + 8 * h) = v;
+    }
+  }
+}
+
 __device__ __forceinline__ i32x4 staged(const char* wl, int q, int c) {
   return *(const i32x4*)(wl + staged_off(q, c));
 }

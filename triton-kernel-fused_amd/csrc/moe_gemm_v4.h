@@ -29,8 +29,10 @@ constexpr int TILE = 256;
 constexpr int WP = 128;          // P rows (MFMA A side, output channels) per wave
 constexpr int WQ = TILE / (NW / 2);  // Q rows (MFMA B side, tokens) per wave
 constexpr int RPW = TILE / NW;   // operand rows (Kc) or K rows x 4 (Rc) each wave loads per slot
-constexpr int TI = WP / 32;      // 4
+constexpr int TI = WP / 32;      // 4   (32x32 MFMA tiles: fp8)
 constexpr int TJ = WQ / 32;      // 2
+constexpr int TI16 = WP / 16;    // 8   (16x16x32 MFMA tiles: 16-bit operands)
+constexpr int TJ16 = WQ / 16;    // 4
 constexpr int OPB = TILE * ROWB; // 32 KB: one operand's K step
 constexpr int LOADS = TILE / NW / 8;  // DMA instructions per wave per operand per step (4)
 
@@ -43,25 +45,28 @@ __device__ __forceinline__ int wave_c() { return wave_id() >> 1; }
 // ---------------------------------------------------------------------------------------------
 // Operand loaders. Each fills one ring slot (one operand's 64-value K step, 32 KB) with four DMA
 // instructions per wave (issue) and reads MFMA operand fragments from a slot (frag): fragment t
-// (< NT_ rows-of-32 of this wave's block), slab sl (16 K values), chunk c (< CPL).
+// (FR rows of this wave's block), slab sl, chunk c (< CPL). FR = 32 (32x32 MFMAs): lane l holds
+// row l%32 and the K chunk l/32 of a 16-value (16-bit) or 64-value (fp8, CPL = 2) slab. FR = 16
+// (16x16x32 MFMAs, 16-bit only): lane l holds row l%16 and K chunk l/16 of a 32-value slab.
 
 // K-contiguous operand: [256 rows][128 bytes], chunk index XOR-ed by (row >> 1) & 7. Lane l of
 // wave w fills row R = 32w + 8i + l/8 (i < 4), physical chunk l%8, i.e. logical chunk
 // (l%8) ^ ((R >> 1) & 7) = (l%8) ^ ((4*(i&1) + l/16) & 7).
-struct KcLoad {
+template <int FR>
+struct KcLoadT {
   const char* rowp[LOADS];  // this lane's rows (clamped to a valid row when outside the operand)
   int cbyte[2];             // byte offset of this lane's logical chunk for even / odd i
-  int fbase;                // fragment reads: byte offset of row rbase + (l & 31)
-  int half, sw;
+  int fbase;                // fragment reads: byte offset of row rbase + l % FR
+  int half, sw;             // K chunk of the lane within a slab (l / FR); swizzle of its rows
 
   // rbase: first operand row of this wave's fragment block.
   __device__ __forceinline__ void init(int rbase) {
     const int l = lane_id();
     cbyte[0] = ((l & 7) ^ (l >> 4)) << 4;
     cbyte[1] = ((l & 7) ^ ((4 + (l >> 4)) & 7)) << 4;
-    fbase = (rbase + (l & 31)) * ROWB;
-    half = l >> 5;
-    sw = (l >> 1) & 7;
+    fbase = (rbase + (l & (FR - 1))) * ROWB;
+    half = l / FR;
+    sw = (l >> 1) & 7;  // ((row >> 1) & 7) for row = rbase + 16u + l % FR (rbase % 16 == 0)
   }
   __device__ __forceinline__ static int row_of(int i) {
     return ((int)threadIdx.x >> 6) * RPW + i * 8 + (lane_id() >> 3);
@@ -82,10 +87,13 @@ struct KcLoad {
   __device__ __forceinline__ void issue_done(int) {}
   template <int CPL>
   __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int c) const {
-    const int cb = (((2 * sl + half) * CPL + c) ^ sw) << 4;
-    return *(const i32x4*)(slot + fbase + t * 32 * ROWB + cb);
+    static_assert(FR == 32 || CPL == 1, "16-row fragments are for 16-bit operands");
+    const int cb = ((((64 / FR) * sl + half) * CPL + c) ^ sw) << 4;
+    return *(const i32x4*)(slot + fbase + t * FR * ROWB + cb);
   }
 };
+using KcLoad = KcLoadT<32>;
+using KcLoad16 = KcLoadT<16>;
 
 // Row-contiguous operand (element (r, k) at src + row(k) * ld + 2r, src at column r0; row(k) =
 // gather[k] or k): [64 K rows][256 r x 2 bytes], the 16-byte chunk index XOR-ed by 4 * (k & 3)
@@ -97,8 +105,12 @@ struct KcLoad {
 // 32-lane half reads 4 K rows x 64 bytes and the XOR puts them on disjoint banks. Lane l of wave w
 // fills K row 8w + 2i + h (h = l/32), physical chunk l%32, i.e. logical chunk
 // (l%32) ^ 4*((2i + h) & 3) = columns 8c .. 8c+7. K values at or past kend read a zero block.
+// FR = 32: the two 16-lane groups of a 32-lane half take columns 16G .. 16G+15 of the fragment
+// and the halves K rows 8h .. 8h+7 of a 16-row slab; FR = 16: the four 16-lane groups g take the
+// fragment's 16 columns and K rows 8g .. 8g+7 of a 32-row slab, and the chunk XOR also takes
+// (k >> 3) & 3 (= g), so the four groups of one read land on different banks.
 constexpr int RC_ROWB = TILE * 2;  // 512 bytes per K row
-template <bool GATHER, int NFRAG>
+template <bool GATHER, int NFRAG, int FR = 32>
 struct RcLoad {
   const char* src;
   size_t ld;
@@ -112,17 +124,24 @@ struct RcLoad {
   // rbase: first column (r) of this wave's fragment block; rvalid: columns inside the operand.
   __device__ __forceinline__ void init(int rbase, int rvalid) {
     const int l = lane_id(), h = l >> 5;
+    // FR = 16 also XORs (k >> 3) & 3 (= w & 3 for this wave's K rows 8w .. 8w+7 of a step).
+    const int wx = FR == 16 ? (wave_id() & 3) : 0;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
-      const int c = (l & 31) ^ (4 * ((2 * par + h) & 3));
+      const int c = (l & 31) ^ (4 * ((2 * par + h) & 3)) ^ wx;
       cbyte[par] = min(8 * c, rvalid - 8) * 2;
       zoff[par] = c * 16;
     }
     const int G = (l >> 4) & 1, j = l & 15, q = j >> 2, p = j & 3;
 #pragma unroll
-    for (int t = 0; t < NFRAG; ++t)
-      toff[t] = (8 * h + q) * RC_ROWB + ((((rbase >> 3) + 4 * t + 2 * G + (p >> 1)) ^ (4 * q)) * 16) +
-                8 * (p & 1);
+    for (int t = 0; t < NFRAG; ++t) {
+      if constexpr (FR == 32)
+        toff[t] = (8 * h + q) * RC_ROWB +
+                  ((((rbase >> 3) + 4 * t + 2 * G + (p >> 1)) ^ (4 * q)) * 16) + 8 * (p & 1);
+      else
+        toff[t] = (8 * (l >> 4) + q) * RC_ROWB +
+                  ((((rbase >> 3) + 2 * t + (p >> 1)) ^ (4 * q) ^ (l >> 4)) * 16) + 8 * (p & 1);
+    }
   }
   __device__ __forceinline__ void fetch_rows(int k) {
     if constexpr (GATHER) {
@@ -155,7 +174,7 @@ struct RcLoad {
   __device__ __forceinline__ i32x4 frag(const char* slot, int t, int sl, int) const {
     typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s4;
     typedef __attribute__((address_space(3))) s4 lds_s4;
-    const char* p0 = slot + toff[t] + sl * 16 * RC_ROWB;
+    const char* p0 = slot + toff[t] + sl * (FR == 32 ? 16 : 32) * RC_ROWB;
     const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p0);
     const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0 + 4 * RC_ROWB));
     typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i2;
@@ -203,16 +222,20 @@ __device__ __forceinline__ void wait_slots(int n) {
 // than issuing them in bursts. Refills past the end re-read the last K step into slots nobody
 // reads again, and the prologue fills the slots the same way at every K length, so every wait is
 // a constant; the loop end waits for all DMAs.
-#ifndef V4_FP8_ROLL
-#define V4_FP8_ROLL 1
-#endif
-template <typename T, class LP, class LQ>
-__device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ& lq, int k0, int k1,
+template <typename T, typename AccV, int TI_, int TJ_, class LP, class LQ>
+__device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ& lq, int k0, int k1,
                                               char* smem) {
   constexpr int KS = v2::bk<T>();
   constexpr int CPL = Mfma<T>::CPL;
-  constexpr int SLABS = ROWB / (32 * CPL);
+  constexpr int FR = sizeof(AccV) == sizeof(f32x4) ? 16 : 32;  // MFMA tile rows
+  static_assert(TI_ * FR == WP && TJ_ * FR == WQ, "accumulators cover the wave's block");
+  constexpr int SLABS = ROWB / ((FR == 16 ? 64 : 32) * CPL);
   static_assert(SLABS >= 2, "the mid-step barrier needs at least two slabs per step");
+  // Fragment schedule: 32x32 16-bit tiles double-buffer both operands' fragments and defer the P
+  // refill to the next step (FB == 2); fp8 and 16x16x32 tiles roll the A fragments and
+  // double-buffer B (ROLL), every refill in the synchronising slab.
+  constexpr bool ROLL = FR == 16 || CPL > 1;
+  constexpr int NM = TI_ * TJ_;  // MFMAs per slab
   const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;
 
@@ -220,7 +243,7 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
   lp.prime(k0);
   lq.prime(k0);
   const int klast = k0 + (nk - 1) * KS;
-  constexpr int PRO = CPL == 1 ? NSLOT - 1 : NSLOT;  // 16-bit: P2 goes out with step 0's slab 0
+  constexpr int PRO = ROLL ? NSLOT : NSLOT - 1;  // FB == 2: P2 goes out with step 0's slab 0
   for (int i = 0; i < PRO; ++i) {
     char* slot = smem + i * SLOTB;
     const int k = min(k0 + (i >> 1) * KS, klast);
@@ -232,37 +255,28 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
   int pp_slot = NSLOT - 1, pp_k = min(k0 + 2 * KS, klast);
   bare_barrier();
 
-  // Operand fragments are double-buffered in registers (slab sl+1 read while slab sl's MFMAs run)
-  // for 16-bit operands; fp8 fragments are twice as large, so they are single-buffered (the
-  // other wave of the SIMD covers the read latency).
-  constexpr int FB = CPL > 1 ? 1 : 2;
-  i32x4 a[FB][TI][CPL], b[FB][TJ][CPL];
+  constexpr int FB = ROLL ? 1 : 2;
+  i32x4 a[FB][TI_][CPL], b[FB][TJ_][CPL];
   auto load = [&](int f, const char* ps, const char* qs, int sl) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-      for (int t = 0; t < TI; ++t) a[f][t][c] = lp.template frag<CPL>(ps, t, sl, c);
+      for (int t = 0; t < TI_; ++t) a[f][t][c] = lp.template frag<CPL>(ps, t, sl, c);
 #pragma unroll
-      for (int t = 0; t < TJ; ++t) b[f][t][c] = lq.template frag<CPL>(qs, t, sl, c);
+      for (int t = 0; t < TJ_; ++t) b[f][t][c] = lq.template frag<CPL>(qs, t, sl, c);
     }
   };
-  auto mfmas = [&](int f) {
-#pragma unroll
-    for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) Mfma<T>::stepf(acc[ti][tj], a[f][ti], b[f][tj]);
-  };
-  // fp8 rolled fragments (V4_FP8_ROLL): one A buffer, two B buffers.
-  i32x4 ra[TI][CPL], rb[2][TJ][CPL];
+  // ROLL: one A buffer, two B buffers.
+  i32x4 ra[TI_][CPL], rb[2][TJ_][CPL];
   int sp = 0, sq = 1;  // slots of P_s, Q_s
   if constexpr (FB == 2) load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
-  if constexpr (FB == 1 && V4_FP8_ROLL) {
+  if constexpr (ROLL) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-      for (int t = 0; t < TI; ++t) ra[t][c] = lp.template frag<CPL>(smem, t, 0, c);
+      for (int t = 0; t < TI_; ++t) ra[t][c] = lp.template frag<CPL>(smem, t, 0, c);
 #pragma unroll
-      for (int t = 0; t < TJ; ++t) rb[0][t][c] = lq.template frag<CPL>(smem + SLOTB, t, 0, c);
+      for (int t = 0; t < TJ_; ++t) rb[0][t][c] = lq.template frag<CPL>(smem + SLOTB, t, 0, c);
     }
     // lgkmcnt(0) (vmcnt and expcnt at their maxima) as a real waitcnt instruction, so the
     // compiler's loop-entry state holds no LDS reads and the in-loop waits stay partial.
@@ -275,56 +289,12 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
     const int nq = sq + 2 >= NSLOT ? sq + 2 - NSLOT : sq + 2;
 #pragma unroll
     for (int sl = 0; sl < SLABS; ++sl) {
-      if constexpr (FB == 2) {
-        const int f = sl & 1;
-        if (sl + 1 == SLABS) {
-          // Synchronisation step, the same at every step (no branches around the MFMAs): wait for
-          // step s+1, barrier, read its first slab, and issue the Q refill one DMA per two MFMAs;
-          // the P refill goes out over the next step's first two slabs. Past the last
-          // step the refills re-read the last K step into slots that are never read again, and
-          // the reads of "step s+1" read stale LDS into unused registers; the loop end drains the
-          // DMAs.
-          wait_slots(1);
-          bare_barrier();
-          load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
-          const int kq = min(k0 + (s + 2) * KS, klast), kp = min(k0 + (s + 3) * KS, klast);
-          char* qslot = smem + sp * SLOTB;
-          __builtin_amdgcn_sched_barrier(0);
-          static_assert(TI * TJ == 2 * LOADS, "one refill DMA per two MFMAs");
-          static_for<0, TI * TJ>([&](auto ic) {
-            constexpr int I = decltype(ic)::value;
-            Mfma<T>::step(acc[I / TJ][I % TJ], a[f][I / TJ][0], b[f][I % TJ][0]);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (I % 2 == 1) lq.template issue_i<T, I / 2>(qslot, kq);
-            __builtin_amdgcn_sched_barrier(0);
-          });
-          lq.issue_done(kq);
-          pp_slot = sq;
-          pp_k = kp;
-        } else {
-          // Next slab's fragment reads (and, in slabs 0 and 1, the pending P refill) between the
-          // MFMAs.
-          static_for<0, TI * TJ>([&](auto ic) {
-            constexpr int I = decltype(ic)::value;
-            if constexpr (I < TI) a[f ^ 1][I][0] = lp.template frag<CPL>(ps, I, sl + 1, 0);
-            else if constexpr (I < TI + TJ) b[f ^ 1][I - TI][0] = lq.template frag<CPL>(qs, I - TI, sl + 1, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            Mfma<T>::step(acc[I / TJ][I % TJ], a[f][I / TJ][0], b[f][I % TJ][0]);
-            __builtin_amdgcn_sched_barrier(0);
-            if constexpr (I % 4 == 3) {
-              if (sl == 0) lp.template issue_i<T, I / 4>(smem + pp_slot * SLOTB, pp_k);
-              if (sl == 1) lp.template issue_i<T, 2 + I / 4>(smem + pp_slot * SLOTB, pp_k);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-          });
-          if (sl == 1) lp.issue_done(pp_k);
-        }
-      } else if constexpr (V4_FP8_ROLL) {
-        // fp8: B fragments double-buffered (the next slab's reads after the slab's first MFMAs), A fragments
-        // rolled: each is re-read for the next slab right after its last MFMA of this slab, so
-        // every read has the rest of the slab's MFMAs to land, within the register budget of one
-        // buffer. The synchronising slab waits, barriers, then reads step s+1's first slab the
-        // same way and issues the refills one DMA per MFMA.
+      if constexpr (ROLL) {
+        // B fragments double-buffered (the next slab's reads after the slab's first MFMAs), A
+        // fragments rolled: each is re-read for the next slab right after its last MFMA of this
+        // slab, so every read has the rest of the slab's MFMAs to land, within the register
+        // budget of one buffer. The synchronising slab waits, barriers, then reads step s+1's
+        // first slab the same way and issues both refills, one DMA per NM / 8 MFMAs.
         const int f = sl & 1;
         const bool sync = sl + 1 == SLABS;
         const char* nps = sync ? smem + np * SLOTB : ps;
@@ -339,24 +309,29 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
           kq = min(k0 + (s + 2) * KS, klast);
           kp = min(k0 + (s + 3) * KS, klast);
         }
+        constexpr int DI = NM / (2 * LOADS);
+        static_assert(DI * 2 * LOADS == NM, "refill DMAs spread evenly over the slab");
         __builtin_amdgcn_sched_barrier(0);
-        static_for<0, TI * TJ>([&](auto ic) {
+        static_for<0, NM>([&](auto ic) {
           constexpr int I = decltype(ic)::value;
-          Mfma<T>::stepf(acc[I / TJ][I % TJ], ra[I / TJ], rb[f][I % TJ]);
+          Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (I < TJ) {
+          if constexpr (I < TJ_) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) rb[f ^ 1][I][c] = lq.template frag<CPL>(nqs, I, nsl, c);
           }
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (I % TJ == TJ - 1) {
+          if constexpr (I % TJ_ == TJ_ - 1) {
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) ra[I / TJ][c] = lp.template frag<CPL>(nps, I / TJ, nsl, c);
+            for (int c = 0; c < CPL; ++c) ra[I / TJ_][c] = lp.template frag<CPL>(nps, I / TJ_, nsl, c);
           }
           __builtin_amdgcn_sched_barrier(0);
-          if (sync) {
-            if constexpr (I < LOADS) lq.template issue_i<T, I>(qslot, kq);
-            else lp.template issue_i<T, I - LOADS>(pslot, kp);
+          if constexpr (I % DI == DI - 1) {
+            constexpr int d = I / DI;
+            if (sync) {
+              if constexpr (d < LOADS) lq.template issue_i<T, d>(qslot, kq);
+              else lp.template issue_i<T, d - LOADS>(pslot, kp);
+            }
           }
           __builtin_amdgcn_sched_barrier(0);
         });
@@ -365,30 +340,48 @@ __device__ __forceinline__ void mainloop_ring(f32x16 (&acc)[TI][TJ], LP& lp, LQ&
           lp.issue_done(kp);
         }
       } else {
-        load(0, ps, qs, sl);
+        const int f = sl & 1;
         if (sl + 1 == SLABS) {
-          // As for 16-bit operands, with single-buffered fragments: the barrier also waits for
-          // this slab's fragment reads before the slots are refilled.
+          // Synchronisation step, the same at every step (no branches around the MFMAs): wait for
+          // step s+1, barrier, read its first slab, and issue the Q refill one DMA per two MFMAs;
+          // the P refill goes out over the next step's first two slabs. Past the last
+          // step the refills re-read the last K step into slots that are never read again, and
+          // the reads of "step s+1" read stale LDS into unused registers; the loop end drains the
+          // DMAs.
           wait_slots(1);
           bare_barrier();
+          load(f ^ 1, smem + np * SLOTB, smem + nq * SLOTB, 0);
           const int kq = min(k0 + (s + 2) * KS, klast), kp = min(k0 + (s + 3) * KS, klast);
           char* qslot = smem + sp * SLOTB;
-          char* pslot = smem + sq * SLOTB;
           __builtin_amdgcn_sched_barrier(0);
-          static_assert(TI * TJ == 2 * LOADS, "one refill DMA per MFMA");
-          static_for<0, TI * TJ>([&](auto ic) {
+          static_assert(NM == 2 * LOADS, "one refill DMA per two MFMAs");
+          static_for<0, NM>([&](auto ic) {
             constexpr int I = decltype(ic)::value;
-            Mfma<T>::stepf(acc[I / TJ][I % TJ], a[0][I / TJ], b[0][I % TJ]);
+            Mfma<T>::step(acc[I / TJ_][I % TJ_], a[f][I / TJ_][0], b[f][I % TJ_][0]);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (I < LOADS) lq.template issue_i<T, I>(qslot, kq);
-            else lp.template issue_i<T, I - LOADS>(pslot, kp);
+            if constexpr (I % 2 == 1) lq.template issue_i<T, I / 2>(qslot, kq);
             __builtin_amdgcn_sched_barrier(0);
           });
           lq.issue_done(kq);
-          lp.issue_done(kp);
+          pp_slot = sq;
+          pp_k = kp;
         } else {
-          __builtin_amdgcn_sched_barrier(0);
-          mfmas(0);
+          // Next slab's fragment reads (and, in slabs 0 and 1, the pending P refill) between the
+          // MFMAs.
+          static_for<0, NM>([&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            if constexpr (I < TI_) a[f ^ 1][I][0] = lp.template frag<CPL>(ps, I, sl + 1, 0);
+            else if constexpr (I < TI_ + TJ_) b[f ^ 1][I - TI_][0] = lq.template frag<CPL>(qs, I - TI_, sl + 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            Mfma<T>::step(acc[I / TJ_][I % TJ_], a[f][I / TJ_][0], b[f][I % TJ_][0]);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (I % 4 == 3) {
+              if (sl == 0) lp.template issue_i<T, I / 4>(smem + pp_slot * SLOTB, pp_k);
+              if (sl == 1) lp.template issue_i<T, 2 + I / 4>(smem + pp_slot * SLOTB, pp_k);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          });
+          if (sl == 1) lp.issue_done(pp_k);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
