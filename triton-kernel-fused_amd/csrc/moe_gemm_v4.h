@@ -1,6 +1,7 @@
 // Grouped GEMM, fourth generation (16-bit operands, both K-contiguous): 256x256 output tile per
-// workgroup of EIGHT waves, two per SIMD. Each wave owns a 128 (P) x 64 (Q) sub-tile: 4 x 2 MFMA
-// 32x32x16 tiles, 128 accumulators per lane, so two waves fit one SIMD's register file.
+// workgroup of EIGHT waves, two per SIMD. Each wave owns a 128 (P) x 64 (Q) sub-tile: 8 x 4 MFMA
+// 16x16x32 tiles (token GEMMs) or 4 x 2 32x32x16 / 32x32x64-fp8 tiles (weight gradients, fp8),
+// 128 accumulators per lane either way, so two waves fit one SIMD's register file.
 //
 // Why eight waves: with one wave per SIMD, every LDS-read wait and barrier of that wave idles its
 // SIMD's MFMA pipe; with two, the other wave's MFMAs fill the gap. Measured on the config-3 gate/up
