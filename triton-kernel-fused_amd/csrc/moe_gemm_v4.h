@@ -109,7 +109,8 @@ using KcLoad16 = KcLoadT<16>;
 // FR = 32: the two 16-lane groups of a 32-lane half take columns 16G .. 16G+15 of the fragment
 // and the halves K rows 8h .. 8h+7 of a 16-row slab; FR = 16: the four 16-lane groups g take the
 // fragment's 16 columns and K rows 8g .. 8g+7 of a 32-row slab, and the chunk XOR also takes
-// (k >> 3) & 3 (= g), so the four groups of one read land on different banks.
+// 2 * ((k >> 3) & 3) (= 2g): a 32-lane half (g, g+1) then varies chunk bits 0 (p), 1 (g) and
+// 2-3 (q) and covers the 64 banks once.
 constexpr int RC_ROWB = TILE * 2;  // 512 bytes per K row
 template <bool GATHER, int NFRAG, int FR = 32>
 struct RcLoad {
@@ -125,8 +126,8 @@ struct RcLoad {
   // rbase: first column (r) of this wave's fragment block; rvalid: columns inside the operand.
   __device__ __forceinline__ void init(int rbase, int rvalid) {
     const int l = lane_id(), h = l >> 5;
-    // FR = 16 also XORs (k >> 3) & 3 (= w & 3 for this wave's K rows 8w .. 8w+7 of a step).
-    const int wx = FR == 16 ? (wave_id() & 3) : 0;
+    // FR = 16 also XORs 2 * ((k >> 3) & 3) (k >> 3 = w for this wave's K rows 8w .. 8w+7).
+    const int wx = FR == 16 ? 2 * (wave_id() & 3) : 0;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
       const int c = (l & 31) ^ (4 * ((2 * par + h) & 3)) ^ wx;
@@ -141,7 +142,7 @@ struct RcLoad {
                   ((((rbase >> 3) + 4 * t + 2 * G + (p >> 1)) ^ (4 * q)) * 16) + 8 * (p & 1);
       else
         toff[t] = (8 * (l >> 4) + q) * RC_ROWB +
-                  ((((rbase >> 3) + 2 * t + (p >> 1)) ^ (4 * q) ^ (l >> 4)) * 16) + 8 * (p & 1);
+                  ((((rbase >> 3) + 2 * t + (p >> 1)) ^ (4 * q) ^ (2 * (l >> 4))) * 16) + 8 * (p & 1);
     }
   }
   __device__ __forceinline__ void fetch_rows(int k) {
