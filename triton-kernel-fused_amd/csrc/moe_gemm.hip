@@ -623,8 +623,8 @@ token_gemm_v4_kernel(TokenArgs a, int n_logical) {
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
-  const int mt = lid / a.n_rtiles;
-  const int rt = lid % a.n_rtiles;
+  int mt, rt;
+  v4::tile_of(lid, a.n_rtiles, mt, rt);
   if (mt >= s_pref[a.E_glu]) return;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
@@ -744,8 +744,8 @@ token_gemm_v3_kernel(TokenArgs a, int n_logical) {
   // The expert tile scan borrows the last LDS stage (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v3::NSTAGE - 1) * v3::STAGEB);
   tile_prefix<v3::NT>(a.offsets, a.E_glu, v3::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
-  const int mt = lid / a.n_rtiles;
-  const int rt = lid % a.n_rtiles;
+  int mt, rt;
+  v4::tile_of(lid, a.n_rtiles, mt, rt);
   if (mt >= s_pref[a.E_glu]) return;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
@@ -845,7 +845,7 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   a.n_rtiles = EPI == EPI_GLU_FWD ? (int)((a.I + v2::TILE / 2 - 1) / (v2::TILE / 2))
                                   : (int)((a.R + v2::TILE - 1) / v2::TILE);
   const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
-  const int64_t logical = max_mt * a.n_rtiles;
+  const int64_t logical = v4::logical_tiles(max_mt, a.n_rtiles);
   if (logical <= 0 || n_rows == 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;

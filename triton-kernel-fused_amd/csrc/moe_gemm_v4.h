@@ -400,5 +400,27 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
 // Block -> logical tile with XCD grouping (see v2::xcd_logical).
 using v2::xcd_logical;
 
+// Logical tile -> (token tile mt, weight tile rt) of a token GEMM. Up to 8 weight tiles: row-major
+// (rt fastest), so the 32 workgroups an XCD runs at once (32 consecutive logical tiles) cover 4+
+// token tiles x every weight tile. More weight tiles: groups of TGM token tiles with the token tile
+// fastest inside a group, so those 32 workgroups cover 8 token tiles x 4 weight tiles (12 operand
+// blocks for the XCD's L2) instead of 2-3 x 12-16 (15-18 blocks); measured +2% on the fp8 forward
+// (12 and 16 weight tiles), -1% when applied to 8 weight tiles.
+constexpr int TGM = 8;
+__host__ __device__ inline int tile_group(int n_rt) { return n_rt > 8 ? TGM : 1; }
+__device__ __forceinline__ void tile_of(int lid, int n_rt, int& mt, int& rt) {
+  const int gm = tile_group(n_rt);
+  const int per = gm * n_rt;
+  const int g = lid / per, w = lid - g * per;
+  mt = g * gm + w % gm;
+  rt = w / gm;
+}
+// Logical tiles to launch for up to max_mt token tiles: whole groups, so every valid (mt, rt)
+// has a logical index below the count.
+inline int64_t logical_tiles(int64_t max_mt, int n_rt) {
+  const int gm = tile_group(n_rt);
+  return (max_mt + gm - 1) / gm * gm * n_rt;
+}
+
 }  // namespace v4
 }  // namespace moe
