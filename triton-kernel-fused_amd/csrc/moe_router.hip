@@ -4,9 +4,10 @@
 // per-expert pick counts for auxiliary-loss-free load balancing; its backward; and the bias update
 // (kernels/sm75/router.py:40-150,152-170,293-301).
 //
-// One wave owns one token row: lane l holds experts l, l+64, ... (EJ per lane), so a top-k step is
-// a per-lane argmax over its EJ values and a 6-step butterfly over the wave that carries
-// (selection value, expert, score). Ties pick the lowest expert index. Counts are summed per
+// One wave owns one token row: lane l holds experts l, l+64, ... (EJ per lane). The top-k is a
+// radix select over distinct integer keys (selection value, then the lower expert index first) by
+// wave ballots: about 40 ballot rounds per row instead of an O(E) scan per lane, then each pick's
+// slot is the count of larger picks. Ties pick the lowest expert index. Counts are summed per
 // workgroup in LDS and added to the global counters with one integer atomic per expert, so the
 // totals do not depend on the order of the atomics.
 #include <algorithm>
@@ -18,26 +19,13 @@ namespace moe {
 constexpr int RT_THREADS = 256;  // 4 waves = 4 token rows per workgroup
 constexpr int RT_MAX_E = 1024;
 constexpr int RT_MAX_K = 32;
-constexpr int RT_RANK_E = 256;   // rank selection for E <= 256 (one LDS row per wave)
-constexpr int RT_MAX_GRID = 1 << 20;  // forward workgroups (grid-stride over rows beyond)
+#ifndef RT_FWD_GRID
+#define RT_FWD_GRID 2048
+#endif
+constexpr int RT_MAX_GRID = RT_FWD_GRID;  // forward workgroups (grid-stride over rows beyond)
 constexpr int RT_COUNT_GRID = 64;    // count workgroups
 
 __device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-// Wave butterfly: the larger selection value wins, ties go to the lower expert index.
-__device__ __forceinline__ void argmax_wave(float& v, int& e, float& s) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float ov = __shfl_xor(v, d, 64);
-    const int oe = __shfl_xor(e, d, 64);
-    const float os = __shfl_xor(s, d, 64);
-    if (ov > v || (ov == v && oe < e)) {
-      v = ov;
-      e = oe;
-      s = os;
-    }
-  }
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -90,95 +78,102 @@ __global__ void __launch_bounds__(RT_THREADS)
 router_fwd_kernel(const T* __restrict__ logits, int64_t ld, int64_t N, int E,
                   const float* __restrict__ bias, int top_k, int softmax, int norm, float scale,
                   int64_t* __restrict__ idx_out, float* __restrict__ w_out) {
-  __shared__ __attribute__((aligned(16))) float s_sel[(RT_THREADS / 64) * RT_RANK_E];
+  __shared__ unsigned long long s_keys[(RT_THREADS / 64) * RT_MAX_K];
   const int lane = threadIdx.x & 63;
+  // Selection keys: the selection value as an order-preserving unsigned integer, then the
+  // complemented expert index in the low ib bits, so keys are distinct and a larger key is the
+  // better pick (ties in value go to the lower expert index). Invalid experts: key 0.
+  const int ib = E > 1 ? 32 - __clz(E - 1) : 0;
+  float bv[EJ];
+#pragma unroll
+  for (int j = 0; j < EJ; ++j) {
+    const int e = lane + 64 * j;
+    bv[j] = bias && e < E ? bias[e] : 0.f;
+  }
   // Grid-stride over rows; the next row's logits are loaded while this row is processed.
   const int64_t step = (int64_t)gridDim.x * (RT_THREADS / 64);
   int64_t n = (int64_t)blockIdx.x * (RT_THREADS / 64) + (threadIdx.x >> 6);
   float xn[EJ];
   if (n < N) row_load<T, EJ>(logits + n * ld, E, lane, xn);
   for (; n < N; n += step) {
-    float s[EJ], sel[EJ], x[EJ];
+    float s[EJ], x[EJ];
 #pragma unroll
     for (int j = 0; j < EJ; ++j) x[j] = xn[j];
     if (n + step < N) row_load<T, EJ>(logits + (n + step) * ld, E, lane, xn);
     row_scores_of<EJ>(x, E, softmax, lane, s);
+    unsigned long long key[EJ];
 #pragma unroll
     for (int j = 0; j < EJ; ++j) {
       const int e = lane + 64 * j;
-      sel[j] = e < E ? s[j] + (bias ? bias[e] : 0.f) : -INFINITY;
+      const unsigned u = __float_as_uint(s[j] + bv[j]);
+      const unsigned k32 = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+      key[j] = e < E ? ((unsigned long long)k32 << ib) | (unsigned long long)(E - 1 - e) : 0ull;
     }
-    if constexpr (EJ <= 4) {
-      // Rank selection: every lane counts, for each of its experts, the experts that beat it
-      // (larger value, or equal value and lower index) over the row's values in LDS; ranks below
-      // top_k are the picks, in order.
-      float* sb = s_sel + (threadIdx.x >> 6) * RT_RANK_E;
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // previous row's reads are done
+    // Bits above the highest one in which two valid keys differ are common to all of them: the
+    // threshold starts with them (two wave reductions on the vector side instead of one scalar
+    // round per bit).
+    unsigned kmax = 0, kmin = 0xffffffffu;
 #pragma unroll
-      for (int j = 0; j < EJ; ++j)
-        if (lane + 64 * j < E) sb[lane + 64 * j] = sel[j];
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the row is in LDS for every lane
-      int rank[EJ];
-#pragma unroll
-      for (int j = 0; j < EJ; ++j) rank[j] = 0;
-#pragma unroll 4
-      for (int e4 = 0; e4 < E; e4 += 4) {
-        const f32x4 v = *(const f32x4*)(sb + e4);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int eo = e4 + u;
-#pragma unroll
-          for (int j = 0; j < EJ; ++j) {
-            const int e = lane + 64 * j;
-            rank[j] += (eo < E) & ((v[u] > sel[j]) | ((v[u] == sel[j]) & (eo < e)));
-          }
-        }
+    for (int j = 0; j < EJ; ++j)
+      if (lane + 64 * j < E) {
+        const unsigned k32 = (unsigned)(key[j] >> ib);
+        kmax = max(kmax, k32);
+        kmin = min(kmin, k32);
       }
-      float tsum = 0.f;
 #pragma unroll
-      for (int j = 0; j < EJ; ++j)
-        if (lane + 64 * j < E && rank[j] < top_k) tsum += s[j];
-      tsum = wave_add(tsum);
-      const float f = norm ? scale / (tsum + 1e-20f) : scale;
-#pragma unroll
-      for (int j = 0; j < EJ; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && rank[j] < top_k) {
-          idx_out[n * top_k + rank[j]] = e;
-          w_out[n * top_k + rank[j]] = s[j] * f;
-        }
-      }
-    } else {
-    // Lane k keeps pick k (every lane sees the same winner after the butterfly).
-    float my_w = 0.f, tsum = 0.f;
-    int my_e = 0;
-#pragma unroll 1
-    for (int k = 0; k < top_k; ++k) {
-      // This lane's best (first maximum in expert order), then the wave's.
-      float v = -INFINITY, sc = 0.f;
-      int e = 0x7fffffff;
-#pragma unroll
-      for (int j = 0; j < EJ; ++j)
-        if (sel[j] > v) {
-          v = sel[j];
-          e = lane + 64 * j;
-          sc = s[j];
-        }
-      argmax_wave(v, e, sc);
-#pragma unroll
-      for (int j = 0; j < EJ; ++j)
-        if (lane + 64 * j == e) sel[j] = -INFINITY;
-      if (lane == k) {
-        my_w = sc;
-        my_e = e;
-      }
-      tsum += sc;
+    for (int d = 32; d >= 1; d >>= 1) {
+      kmax = max(kmax, (unsigned)__shfl_xor((int)kmax, d, 64));
+      kmin = min(kmin, (unsigned)__shfl_xor((int)kmin, d, 64));
     }
+    const int top = kmax == kmin ? -1 : 31 - __clz(kmax ^ kmin);  // highest differing value bit
+    // A threshold that exactly top_k keys reach, one bit at a time from there down: keep a bit
+    // when at least top_k keys reach the threshold with it set, stop as soon as exactly top_k do
+    // (one ballot per bit and expert slot; the threshold is wave-uniform, the counting runs on the
+    // scalar unit, which one CU's four SIMDs share, so the fewer rounds the better).
+    unsigned long long thr =
+        top >= 31 ? 0ull : ((unsigned long long)((kmax >> (top + 1)) << (top + 1)) << ib);
+    for (int b = top + ib; b >= 0; --b) {
+      const unsigned long long c = thr | (1ull << b);
+      int cnt = 0;
+#pragma unroll
+      for (int j = 0; j < EJ; ++j) cnt += __popcll(__ballot(key[j] >= c));
+      if (cnt >= top_k) {
+        thr = c;
+        if (cnt == top_k) break;  // exactly top_k keys reach thr: the lower bits change nothing
+      }
+    }
+    // The picks are the top_k keys >= thr. They are compacted into this wave's LDS row, and a
+    // pick's slot is the number of picked keys larger than its own.
+    unsigned long long* sk = s_keys + (threadIdx.x >> 6) * RT_MAX_K;
+    bool pick[EJ];
+    float tsum = 0.f;
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      pick[j] = key[j] >= thr;
+      tsum += pick[j] ? s[j] : 0.f;
+      const unsigned long long m = __ballot(pick[j]);
+      const int before = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+      if (pick[j]) sk[base + before] = key[j];
+      base += __popcll(m);
+    }
+    int rank[EJ];
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) rank[j] = 0;
+    for (int i = 0; i < top_k; ++i) {
+      const unsigned long long kp = sk[i];
+#pragma unroll
+      for (int j = 0; j < EJ; ++j) rank[j] += kp > key[j];
+    }
+    tsum = wave_add(tsum);
     const float f = norm ? scale / (tsum + 1e-20f) : scale;
-    if (lane < top_k) {
-      idx_out[n * top_k + lane] = my_e;
-      w_out[n * top_k + lane] = my_w * f;
-    }
+#pragma unroll
+    for (int j = 0; j < EJ; ++j) {
+      if (pick[j]) {
+        idx_out[n * top_k + rank[j]] = lane + 64 * j;
+        w_out[n * top_k + rank[j]] = s[j] * f;
+      }
     }
   }
 }
