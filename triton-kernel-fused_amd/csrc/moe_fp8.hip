@@ -31,17 +31,14 @@ struct Fp8Args {
 
 template <bool GLU>
 __global__ void __launch_bounds__(v4::NT, 1)
-fp8_gemm_kernel(Fp8Args a, int n_logical) {
+fp8_gemm_kernel(Fp8Args a) {
   using C = Cfg<fp8e4m3, v4::TILE, v4::TILE, 2, 2>;  // GLU row interleave per 128-row P half
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const int lid = v4::xcd_logical((int)blockIdx.x, (int)gridDim.x);
-  if (lid >= n_logical) return;
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
   int mt, rt;
-  v4::tile_of(lid, a.n_rtiles, mt, rt);
-  if (mt >= s_pref[a.E_glu]) return;
+  if (!v4::block_tile(s_pref[a.E_glu], a.n_rtiles, mt, rt)) return;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -208,7 +205,7 @@ static int launch_fp8(Fp8Args a, int64_t n_rows, hipStream_t s) {
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   auto kern = fp8_gemm_kernel<GLU>;
   (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, (int)logical);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 

@@ -615,17 +615,14 @@ using V4Sh32 = V4Shape<f32x16, v4::TI, v4::TJ, 32, v4::KcLoad>;
 // (P_RC) in the dX GEMMs.
 template <typename T, int EPI, bool P_RC>
 __global__ void __launch_bounds__(v4::NT, 1)
-token_gemm_v4_kernel(TokenArgs a, int n_logical) {
+token_gemm_v4_kernel(TokenArgs a) {
   using C = V2Cfg<T>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const int lid = v4::xcd_logical((int)blockIdx.x, (int)gridDim.x);
-  if (lid >= n_logical) return;
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
   int mt, rt;
-  v4::tile_of(lid, a.n_rtiles, mt, rt);
-  if (mt >= s_pref[a.E_glu]) return;
+  if (!v4::block_tile(s_pref[a.E_glu], a.n_rtiles, mt, rt)) return;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -852,7 +849,7 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   if (a.K % 64 == 0) {
     auto kern = token_gemm_v4_kernel<T, EPI, P_RC>;
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, (int)logical);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a);
   } else {
     if constexpr (P_RC) {
       auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
