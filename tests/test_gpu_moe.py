@@ -235,3 +235,17 @@ def test_bf16_short_k_loops(h, i):
     ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
     mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
     _assert_bf16(mine, ref)
+
+
+@pytest.mark.parametrize("h,i", [(96, 80), (160, 200)])
+def test_bf16_k_not_multiple_of_64(h, i):
+    """K not a multiple of the ring kernels' 64-value step (H = 96 / 160, 2I = 160 / 400): the
+    forwards and the non-gated down-dX take the first-generation kernels, the gate/up dX the
+    five-stage fallback."""
+    codes = [0, 1, 0, 1, 3]
+    hid, idx, w, gu, dw, codes_t, ap, go = _case(codes, 4, dtype=torch.bfloat16, n=300, h=h, i=i,
+                                                 k=2, seed=h * i)
+    _say(f"bf16 K % 64 != 0 h={h} i={i}")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
+    mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
+    _assert_bf16(mine, ref)

@@ -733,17 +733,14 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
 // dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.
 template <typename T, int EPI, bool P_RC>
 __global__ void __launch_bounds__(v3::NT, 1)
-token_gemm_v3_kernel(TokenArgs a, int n_logical) {
+token_gemm_v3_kernel(TokenArgs a) {
   using C = V2Cfg<T>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  const int lid = v3::xcd_logical((int)blockIdx.x, (int)gridDim.x);
-  if (lid >= n_logical) return;
   // The expert tile scan borrows the last LDS stage (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v3::NSTAGE - 1) * v3::STAGEB);
   tile_prefix<v3::NT>(a.offsets, a.E_glu, v3::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
   int mt, rt;
-  v4::tile_of(lid, a.n_rtiles, mt, rt);
-  if (mt >= s_pref[a.E_glu]) return;
+  if (!v4::block_tile(s_pref[a.E_glu], a.n_rtiles, mt, rt)) return;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -854,7 +851,7 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
     if constexpr (P_RC) {
       auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
-      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a, (int)logical);
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a);
     } else {
       return MOE_ERR_SHAPE;  // callers route K % 64 != 0 forwards to the first-generation kernel
     }

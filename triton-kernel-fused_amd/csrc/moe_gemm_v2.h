@@ -316,10 +316,5 @@ __device__ __forceinline__ void store_staged(const char* wl, T* out, long long l
   }
 }
 
-// Block -> logical tile with XCD grouping: workgroups are dealt to the 8 XCDs round-robin, so
-// logical = (b % 8) * (G8 / 8) + b / 8 gives every XCD a contiguous run of logical tiles (shared
-// operands stay in that XCD's L2). G8 = gridDim.x, a multiple of 8.
-__device__ __forceinline__ int xcd_logical(int b, int g8) { return (b & 7) * (g8 >> 3) + (b >> 3); }
-
 }  // namespace v2
 }  // namespace moe

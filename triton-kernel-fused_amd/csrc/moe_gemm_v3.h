@@ -251,7 +251,5 @@ __device__ __forceinline__ void mainloop(f32x16 (&acc)[TN][TN], LP& lp, LQ& lq, 
   lds_barrier();
 }
 
-__device__ __forceinline__ int xcd_logical(int b, int g8) { return (b & 7) * (g8 >> 3) + (b >> 3); }
-
 }  // namespace v3
 }  // namespace moe

@@ -397,9 +397,6 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   bare_barrier();
 }
 
-// Block -> logical tile with XCD grouping (see v2::xcd_logical).
-using v2::xcd_logical;
-
 // Logical tile -> (token tile mt, weight tile rt) of a token GEMM. Up to 8 weight tiles: row-major
 // (rt fastest), so the 32 workgroups an XCD runs at once (32 consecutive logical tiles) cover 4+
 // token tiles x every weight tile. More weight tiles: groups of TGM token tiles with the token tile
