@@ -75,34 +75,58 @@ dispatch_hist_kernel(const int64_t* __restrict__ idx, int64_t M, int E, int32_t*
   if (bad) atomicAdd(status, bad);
 }
 
-// One workgroup. hist (nchunks, E) is rewritten in place into exclusive per-chunk bases.
+// One workgroup. hist (nchunks, E) is rewritten in place into exclusive per-chunk bases. The
+// chunks are cut into G groups (thread g*E + e takes expert e of group g) so the group sums load
+// in parallel; a scan over the groups in LDS gives each group's base.
 __global__ void __launch_bounds__(1024)
 dispatch_scan_kernel(int32_t* __restrict__ hist, int nchunks, int E, int32_t* __restrict__ counts,
                      int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets,
                      int32_t* __restrict__ expert_order) {
   __shared__ int s_cnt[MAX_EXPERTS];
   __shared__ int s_tiles[MAX_EXPERTS];
-  const int e = threadIdx.x;
-  if (e < E) {
-    // Eight chunks' counts are loaded before any is rewritten, so the loads overlap.
-    int run = 0;
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+  __shared__ int s_part[1024];  // [group][expert] chunk-group sums
+  const int G = max(1, min(1024 / E, nchunks));
+  const int g = threadIdx.x / E, e = threadIdx.x % E;
+  const bool act = g < G;
+  const int c_lo = act ? g * nchunks / G : 0, c_hi = act ? (g + 1) * nchunks / G : 0;
+  // Eight chunks' counts are loaded before any is used, so the loads overlap.
+  int sum = 0;
+  for (int c0 = c_lo; c0 < c_hi; c0 += 8) {
+    int v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = c0 + j < c_hi ? hist[(int64_t)(c0 + j) * E + e] : 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[j];
+  }
+  if (act) s_part[g * E + e] = sum;
+  __syncthreads();
+  if (act) {
+    int run = 0, total = 0;
+    for (int gg = 0; gg < G; ++gg) {
+      const int p = s_part[gg * E + e];
+      run += gg < g ? p : 0;
+      total += p;
+    }
+    for (int c0 = c_lo; c0 < c_hi; c0 += 8) {
       int v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = c0 + j < nchunks ? hist[(int64_t)(c0 + j) * E + e] : 0;
+      for (int j = 0; j < 8; ++j) v[j] = c0 + j < c_hi ? hist[(int64_t)(c0 + j) * E + e] : 0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if (c0 + j < nchunks) hist[(int64_t)(c0 + j) * E + e] = run;
+        if (c0 + j < c_hi) hist[(int64_t)(c0 + j) * E + e] = run;
         run += v[j];
       }
     }
-    counts[e] = run;
-    s_cnt[e] = run;
-    s_tiles[e] = (run + TILE_ROWS - 1) / TILE_ROWS;
+    if (g == 0) {
+      counts[e] = total;
+      s_cnt[e] = total;
+      s_tiles[e] = (total + TILE_ROWS - 1) / TILE_ROWS;
+    }
   }
   __syncthreads();
   // Experts by descending count (ties by id): rank = experts that sort before this one.
-  if (e < E) {
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
     const int c = s_cnt[e];
     int rank = 0;
     for (int j = 0; j < E; ++j) {
