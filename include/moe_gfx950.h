@@ -63,6 +63,10 @@ int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int 
  * gate_up[m] = hidden[sorted_token[m]] @ gate_up_proj[e]^T for every sorted row m of a GLU expert
  * e < E_glu; inter[m, i] = act_e(gate) * up (act code 0 = SiLU, 1 = ReLU^2; the two codes the
  * epilogue fuses). inter_out may be NULL: then only gate_up is written (any act code).
+ * top_k_weights non-NULL (model dtype; 16-bit dtypes, H % 64 == 0, inter_out given): inter is the
+ * gate-weighted w * act(gate) * up with w = top_k_weights[sorted_flat[m]], or top_k_weights[m]
+ * when sorted_flat is NULL (gates already in sorted-row order), so the down projection yields
+ * w * eo and moe_combine_fwd with glu_rows_weighted = 1 only sums. NULL: unweighted.
  * Replaces `_grouped_mm` + `_glu_fwd` (kernels/sm75/moe.py:590-591), torch._grouped_mm +
  * BatchedGLU (kernels/sm120/moe_grouped.py:106-107) and the per-expert `@` + `_glu_fwd`
  * (kernels/sm75/moe.py:765-769). */
@@ -70,7 +74,9 @@ int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int64_t n_token
                                   const void* gate_up_proj, int E_glu, int64_t I,
                                   const int32_t* act_codes, const int32_t* offsets,
                                   const int32_t* tile_offsets, const int32_t* sorted_token,
-                                  int64_t n_rows, void* gate_up_out, void* inter_out, void* stream);
+                                  int64_t n_rows, void* gate_up_out, void* inter_out,
+                                  const void* top_k_weights, const int32_t* sorted_flat,
+                                  void* stream);
 
 /* Grouped down projection: eo[m] = inter[m] @ down_proj[e]^T.
  * Replaces `_grouped_mm(inter, down_proj, ...)` (kernels/sm75/moe.py:592), the per-expert
@@ -82,12 +88,13 @@ int moe_grouped_down_fwd(int dtype, const void* inter, const void* down_proj, in
 /* Gate-weighted combine: out[t] = sum_j w[t,j] * row(t,j), fp32 accumulation in slot order, where
  * row = eo[flat_to_sorted[t*k+j]] for GLU experts, hidden[t] for Identity (code 3), nothing for
  * Zero (code 4); experts e >= E_glu are the weightless specials, n_experts = len(act_codes).
+ * glu_rows_weighted = 1: the GLU rows of eo already carry their gate (weight 1 here).
  * Replaces `_combine_scatter` (kernels/sm75/moe.py:673-682,704-709), the grouped
  * index_add_ (:593-595) and kernels/sm120/moe_grouped.py:110-121. Deterministic (no atomics). */
 int moe_combine_fwd(int dtype, const void* eo, const void* hidden, const void* top_k_weights,
                     const int64_t* top_k_indices, const int32_t* act_codes, int n_experts, int E_glu,
                     const int32_t* flat_to_sorted, int64_t n_tokens, int top_k, int64_t H,
-                    void* out, void* stream);
+                    int glu_rows_weighted, void* out, void* stream);
 
 /* Combine backward: grad_eo[m] = grad_out[t] * w (GLU rows), grad_wt[flat] = sum_h grad_out[t,h] *
  * row[h] (fp32 reduction; row = eo[m] for GLU, hidden[t] for Identity, 0 for Zero).
@@ -134,10 +141,12 @@ int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* 
                       void* out, void* stream);
 
 /* Down-projection dX for fused codes (0 SiLU, 1 ReLU^2) with the combine backward folded in.
- * For sorted row m of GLU expert e, token t = sorted_token[m], w = top_k_weights[sorted_flat[m]]:
+ * For sorted row m of GLU expert e, token t = sorted_token[m], w = top_k_weights[sorted_flat[m]]
+ * (sorted_flat NULL: top_k_weights is already in sorted-row order, w = top_k_weights[m]):
  * s = grad_out[t] @ down_proj[e] (grad_out rows gathered, grad_out_ld elements apart);
  * ggu_out[m] = GLU backward of w*s; inter_w_out[m] = w * act(gate)*up (the down weight gradient's
- * row operand, so grad_eo = w*grad_out is never materialised); wt_partial[p*n_rows + m] = the
+ * row operand, so grad_eo = w*grad_out is never materialised; may be NULL when the forward kept
+ * the gate-weighted intermediate); wt_partial[p*n_rows + m] = the
  * partial dot sum over channel slice p of s*inter, p < moe_gate_grad_parts(I).
  * Replaces moe_combine_bwd + moe_grouped_down_dx_swiglu_bwd for these codes: grad_eo = w*go and
  * grad_w = <go, eo> = <go @ W_d, inter> (kernels/sm75/moe.py:606-611,712-720). H % 64 == 0,

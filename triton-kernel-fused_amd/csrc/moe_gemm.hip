@@ -429,9 +429,12 @@ template <typename T> using V2Cfg = Cfg<T, v2::TILE, v2::TILE, 2, 2>;
 //   EPI_GLU_BWD chunk c -> grad_inter channel rt*256 + wr*128 + 8c
 // WQ = token rows per wave; the wave holds channels wr*128..+127
 // of the 256-channel tile and token rows wc*WQ..+WQ-1.
+// wrow (WQ = 64): the gate of token row row0 + lane when a.gate is set (1 otherwise), fetched by
+// the caller before its K loop.
 template <typename T, int EPI, int WQ = 32 * v2::TN, class Acc>
 __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArgs& a, int e, int m0,
-                                                  int m_end, int rt, char* smem, int wr, int wc) {
+                                                  int m_end, int rt, char* smem, int wr, int wc,
+                                                  float wrow = 1.f) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   char* wl = smem + w * (WQ * v2::EPI_ROWB);
   const int row0 = m0 + wc * WQ;
@@ -450,6 +453,9 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
       const int q = i * 8 + (lane >> 3);
       const int m = row0 + q;
       const i32x4 gq = v2::staged(wl, q, c), uq = v2::staged(wl, q, c + 8);
+      // Weighted intermediate (a.gate set): w * act(g) * u, so the down projection yields w * eo
+      // and the combine only sums; w = 1 (exact) otherwise. Shuffled with every lane active.
+      const float w = __shfl(wrow, q & 63, 64);
       if (m < m_end && ch < a.I) {
         T* r = gu + (size_t)m * 2 * a.I + ch;
         v2::st_stream(gq, r);
@@ -459,7 +465,7 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
           v2::unpack8<T>(gq, gv);
           v2::unpack8<T>(uq, uv);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) iv[j] = glu_act(code, gv[j]) * uv[j];
+          for (int j = 0; j < 8; ++j) iv[j] = w * (glu_act(code, gv[j]) * uv[j]);
           v2::st_stream(v2::pack8<T>(iv), it + (size_t)m * a.I + ch);
         }
       }
@@ -474,8 +480,8 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
     const int ch = rt * v2::TILE + wr * v2::WT + 8 * c;
     const int chc = min(ch, a.I - 8);
     const bool cok = ch < a.I;
+    static_assert(WQ == 64, "one gate per lane of the wave's token rows");
     const T* gu = (const T*)a.aux;
-    const T* gw = (const T*)a.gate;
     T* ggu = (T*)a.out;
     T* iw = (T*)a.out2;
     float* part = a.part + (size_t)(2 * rt + wr) * a.out_ld;  // out_ld = M (partials row length)
@@ -490,7 +496,7 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
         const T* r = gu + (size_t)m * 2 * a.I + chc;
         gq[b] = *(const i32x4*)r;
         uq[b] = *(const i32x4*)(r + a.I);
-        wv[b] = to_f32(gw[a.sflat[m]]);
+        wv[b] = __shfl(wrow, (i0 + b) * 4 + (lane >> 4), 64);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -634,6 +640,19 @@ token_gemm_v4_kernel(TokenArgs a) {
   const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
   const int wr = v4::wave_r(), wc = v4::wave_c();
 
+  // Gate of this lane's token row (gated backward; weighted forward intermediate), needed only by
+  // the epilogue, loaded with the token-row indices below. sflat null: the gates are already in
+  // sorted-row order (one load); else indexed through sflat (two dependent loads).
+  // The load is unconditional (a readable dummy address without gates) and its value is first
+  // touched after the K loop, so nothing waits for it before then.
+  constexpr bool WGATE = EPI == EPI_GLU_BWD_GATED || EPI == EPI_GLU_FWD;
+  unsigned short wbits = 0;
+  if constexpr (WGATE) {
+    const int m = min(m0 + wc * v4::WQ + v4::lane_id(), m_end - 1);
+    const unsigned short* gp = (const unsigned short*)a.offsets;
+    if (a.gate) gp = (const unsigned short*)a.gate + (a.sflat ? a.sflat[m] : m);
+    wbits = *gp;
+  }
   // Token rows past the group end read row m0 (their results are never stored).
   typename V4Sh16::Kc lq;
   lq.init(wc * v4::WQ);
@@ -656,7 +675,7 @@ token_gemm_v4_kernel(TokenArgs a) {
     lp.gather = nullptr;
     lp.kend = a.K;
     lp.init(wr * v4::WP, a.R - r0);
-    __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+    v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
     v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
   } else {
     typename V4Sh16::Kc lp;
@@ -674,10 +693,14 @@ token_gemm_v4_kernel(TokenArgs a) {
       }
       lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
     }
-    __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
+    v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
     v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
   }
-  token_epilogue_v2<T, EPI, v4::WQ>(acc, a, e, m0, m_end, rt, smem, wr, wc);
+  float wrow = 1.f;
+  if constexpr (WGATE) {
+    if (a.gate) wrow = to_f32(__builtin_bit_cast(T, wbits));
+  }
+  token_epilogue_v2<T, EPI, v4::WQ>(acc, a, e, m0, m_end, rt, smem, wr, wc, wrow);
 }
 
 // Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
@@ -848,7 +871,7 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a);
   } else {
-    if constexpr (P_RC) {
+    if constexpr (P_RC && EPI != EPI_GLU_BWD_GATED) {  // the gated epilogue needs the v4 kernel
       auto kern = token_gemm_v3_kernel<T, EPI, P_RC>;
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v3::LDSB);
       hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v3::NT), v3::LDSB, s, a);
@@ -916,13 +939,17 @@ extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int6
                                              int64_t I, const int32_t* act_codes,
                                              const int32_t* offsets, const int32_t* tile_offsets,
                                              const int32_t* sorted_token, int64_t n_rows,
-                                             void* gate_up_out, void* inter_out, void* stream) {
+                                             void* gate_up_out, void* inter_out,
+                                             const void* top_k_weights,
+                                             const int32_t* sorted_flat, void* stream) {
   (void)tile_offsets;
   int st = check_common(dtype, H, I, E_glu, n_rows);
   if (st) return st;
   if (n_rows == 0) return MOE_OK;
   if (!hidden || !gate_up_proj || !offsets || !sorted_token || !gate_up_out || !act_codes)
     return MOE_ERR_SHAPE;
+  // Gate-weighted intermediate: 16-bit operands, H a multiple of 64 (the ring kernel's epilogue).
+  if (top_k_weights && (!inter_out || dtype == MOE_DT_F32 || H % 64 != 0)) return MOE_ERR_SHAPE;
   if (!aligned16(hidden) || !aligned16(gate_up_proj) || !aligned16(gate_up_out) ||
       (inter_out && !aligned16(inter_out)))
     return MOE_ERR_ALIGN;
@@ -932,6 +959,7 @@ extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int6
   a.Q = hidden; a.q_ld = H; a.q_gather = sorted_token;
   a.offsets = offsets; a.E_glu = E_glu; a.act_codes = act_codes; a.I = (int)I;
   a.out = gate_up_out; a.out_ld = 2 * I; a.out2 = inter_out;
+  a.gate = top_k_weights; a.sflat = sorted_flat;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {
@@ -1032,7 +1060,7 @@ extern "C" int moe_grouped_down_dx_gated_bwd(int dtype, const void* grad_out, in
   if (H % 64 != 0) return MOE_ERR_ALIGN;
   if (n_rows == 0) return MOE_OK;
   if (!grad_out || !down_proj || !gate_up || !act_codes || !top_k_weights || !offsets ||
-      !sorted_token || !sorted_flat || !wt_partial)
+      !sorted_token || !wt_partial)
     return MOE_ERR_SHAPE;
   if (grad_out_ld < H || grad_out_ld % 8 != 0) return MOE_ERR_ALIGN;
   if (!aligned16(grad_out) || !aligned16(down_proj) || !aligned16(gate_up) ||

@@ -141,14 +141,14 @@ __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T
   }
 }
 
-// out[t] = sum_j w[t,j] * row(t,j)
-template <typename T, int BATCH>
+// out[t] = sum_j w[t,j] * row(t,j); GATE_GLU false: GLU rows already carry their gate.
+template <typename T, bool GATE_GLU>
 __global__ void __launch_bounds__(ROW_THREADS)
 combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
                    const T* __restrict__ wt, const int64_t* __restrict__ idx,
                    const int32_t* __restrict__ codes, int E_glu, int E_all,
                    const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out) {
-  token_gather<T, true, BATCH>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out);
+  token_gather<T, GATE_GLU, 8>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out);
 }
 
 // Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
@@ -441,7 +441,7 @@ extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
                                const void* top_k_weights, const int64_t* top_k_indices,
                                const int32_t* act_codes, int n_experts, int E_glu,
                                const int32_t* flat_to_sorted, int64_t n_tokens, int top_k,
-                               int64_t H, void* out, void* stream) {
+                               int64_t H, int glu_rows_weighted, void* out, void* stream) {
   int st = check_rows(dtype, n_tokens, top_k, H, n_experts, E_glu);
   if (st) return st;
   if (n_tokens == 0) return MOE_OK;
@@ -453,9 +453,14 @@ extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
   if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(row_grid(n_tokens * col_waves));
-  MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, 8, grid, dim3(ROW_THREADS), s,
-                 (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-                 act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
+  if (glu_rows_weighted)
+    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, false, grid, dim3(ROW_THREADS), s,
+                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
+  else
+    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, true, grid, dim3(ROW_THREADS), s,
+                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
+                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 

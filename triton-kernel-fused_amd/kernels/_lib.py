@@ -27,9 +27,10 @@ _SIGS = {
     "moe_tile_rows": [],
     "moe_get_workspace_size": [_L, _I, _I],
     "moe_dispatch": [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
-    "moe_grouped_gateup_swiglu_fwd": [_I, _P, _L, _L, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P, _P],
+    "moe_grouped_gateup_swiglu_fwd": [_I, _P, _L, _L, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P, _P,
+                                      _P, _P],
     "moe_grouped_down_fwd": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
-    "moe_combine_fwd": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
+    "moe_combine_fwd": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _L, _I, _L, _I, _P, _P],
     "moe_combine_bwd": [_I, _P, _L, _P, _P, _P, _P, _P, _I, _I, _P, _P, _L, _I, _L, _P, _P, _P],
     "moe_grouped_down_dx_swiglu_bwd": [_I, _P, _P, _I, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P],
     "moe_grouped_down_dx_gated_bwd": [_I, _P, _L, _P, _I, _L, _L, _P, _P, _P, _P, _P, _P, _L,

@@ -41,7 +41,7 @@ def _combine(eo, wt, idx, routing, n_tok, h, e):
     codes = torch.zeros(e, device=eo.device, dtype=torch.int32)
     _lib.call("moe_combine_fwd", _lib.dtype_code(torch.bfloat16), _lib.ptr(eo), _lib.ptr(eo),
               _lib.ptr(wt), _lib.ptr(idx), _lib.ptr(codes), e, e, _lib.ptr(routing.flat_to_sorted),
-              n_tok, idx.shape[1], h, _lib.ptr(out), _lib.stream_of(eo.device))
+              n_tok, idx.shape[1], h, 0, _lib.ptr(out), _lib.stream_of(eo.device))
     return out
 
 

@@ -182,12 +182,20 @@ class _MoEFunction(torch.autograd.Function):
         inter = torch.empty(m, inter_dim, device=dev, dtype=dt)
         eo = torch.empty(m, h, device=dev, dtype=dt)
         row = None
+        # With the folded backward the saved intermediate is gate-weighted (w * act(g) * u): the
+        # down projection then yields w * eo, the combine only sums, and the backward's down
+        # weight gradient reads it as is.
+        gated = _gated_bwd(fused, e_glu, m, dt, h)
+        # Gates in sorted-row order (one load per row in the GEMM epilogues instead of two). Rows
+        # past the routed count (out-of-range expert ids) hold no index: clamped, never read.
+        w_sorted = (torch.index_select(wt.view(-1), 0, routing.sorted_flat.clamp(0, m - 1))
+                    if gated else None)
         if e_glu > 0 and m > 0:
             _lib.call("moe_grouped_gateup_swiglu_fwd", dtc, _lib.ptr(hidden), n_tok, h,
                       _lib.ptr(gate_up_proj), e_glu, inter_dim, _lib.ptr(codes_t),
                       _lib.ptr(routing.offsets), _lib.ptr(routing.tile_offsets),
                       _lib.ptr(routing.sorted_token), m, _lib.ptr(gate_up),
-                      _lib.ptr(inter) if fused else None, stream)
+                      _lib.ptr(inter) if fused else None, _lib.ptr(w_sorted), None, stream)
             if not fused:
                 row = _row_params(routing, codes_t, ap32, n_exp, m)
                 row_act, ra, rg, _ = row
@@ -200,13 +208,14 @@ class _MoEFunction(torch.autograd.Function):
         out = torch.empty(n_tok, h, device=dev, dtype=dt)
         _lib.call("moe_combine_fwd", dtc, _lib.ptr(eo), _lib.ptr(hidden), _lib.ptr(wt),
                   _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu, _lib.ptr(routing.flat_to_sorted),
-                  n_tok, k, h, _lib.ptr(out), stream)
+                  n_tok, k, h, int(gated), _lib.ptr(out), stream)
 
-        # The folded backward recomputes <grad_out, eo> from inter, so eo need not stay alive.
-        keep_eo = torch.empty(0) if _gated_bwd(fused, e_glu, m, dt, h) else eo
+        # The folded backward recomputes <grad_out, eo> from gate_up, so eo need not stay alive.
+        keep_eo = torch.empty(0) if gated else eo
         ctx.save_for_backward(hidden, idx, wt, gate_up_proj, down_proj, codes_t,
                               ap32 if ap32 is not None else torch.empty(0), gate_up, inter, keep_eo)
         ctx.routing = routing
+        ctx.w_sorted = w_sorted
         ctx.row = row
         ctx.meta = (n_tok, h, inter_dim, k, e_glu, n_exp, fused, ap32 is not None)
         return out
@@ -310,9 +319,11 @@ class _MoEFunction(torch.autograd.Function):
 def _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap):
     """Backward for fused activation codes with the combine backward folded into the down-dX GEMM:
     grad_eo = w * grad_out is never stored; that GEMM gathers grad_out rows itself, applies w in
-    its epilogue, writes w * inter for the down weight gradient and per-slice partials of the gate
-    gradient <grad_out, eo> = <grad_out @ W_d, inter> (kernels/sm75/moe.py:606-617,712-720)."""
-    (hidden, idx, wt, gate_up_proj, down_proj, codes_t, ap32, gate_up, inter,
+    its epilogue and writes per-slice partials of the gate gradient <grad_out, eo> =
+    <grad_out @ W_d, inter> with inter recomputed from gate_up (kernels/sm75/moe.py:606-617,712-720).
+    The forward saved the gate-weighted intermediate w * inter, which is what the down weight
+    gradient sum_m (w inter)^T grad_out needs."""
+    (hidden, idx, wt, gate_up_proj, down_proj, codes_t, ap32, gate_up, inter_w,
      _eo) = ctx.saved_tensors
     n_tok, h, inter_dim, k, e_glu, n_exp, _fused, _has_ap = ctx.meta
     routing = ctx.routing
@@ -327,12 +338,10 @@ def _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap):
     n_parts = _lib.lib().moe_gate_grad_parts(inter_dim)
     part = torch.empty(n_parts, m, device=dev, dtype=torch.float32)
     ggu = torch.empty(m, 2 * inter_dim, device=dev, dtype=dt) if (need_x or need_gu) else None
-    inter_w = torch.empty(m, inter_dim, device=dev, dtype=dt) if need_dw else None
     _lib.call("moe_grouped_down_dx_gated_bwd", dtc, _lib.ptr(go), go_ld, _lib.ptr(down_proj),
-              e_glu, h, inter_dim, _lib.ptr(gate_up), _lib.ptr(codes_t), _lib.ptr(wt),
-              _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token),
-              _lib.ptr(routing.sorted_flat), m, _lib.ptr(ggu), _lib.ptr(inter_w), _lib.ptr(part),
-              stream)
+              e_glu, h, inter_dim, _lib.ptr(gate_up), _lib.ptr(codes_t), _lib.ptr(ctx.w_sorted),
+              _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token), None, m, _lib.ptr(ggu),
+              None, _lib.ptr(part), stream)
     g_wt = g_dw = g_gu = g_x = None
     if need_wt:
         g_wt = torch.empty(n_tok, k, device=dev, dtype=dt)
