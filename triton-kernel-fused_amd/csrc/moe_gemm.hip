@@ -485,7 +485,9 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
     T* ggu = (T*)a.out;
     T* iw = (T*)a.out2;
     float* part = a.part + (size_t)(2 * rt + wr) * a.out_ld;  // out_ld = M (partials row length)
-    constexpr int NB = 8;  // rows per batch of loads
+    // Rows per batch of gate_up loads: 4 measured ~1% faster than 8 and ~4% faster than all 16 at
+    // once (the epilogues of all CUs compete for HBM).
+    constexpr int NB = 4;
 #pragma unroll 1
     for (int i0 = 0; i0 < WQ / 4; i0 += NB) {
       i32x4 gq[NB], uq[NB];
