@@ -1,7 +1,13 @@
 // Grouped expert GEMMs for gfx950: forward gate/up (+GLU epilogue), forward down, backward dX of
-// both projections (+GLU-backward epilogue on the down one) and the ragged weight gradients.
+// both projections (+GLU-backward epilogue on the down one) and the ragged weight gradients; the
+// C-ABI entry points at the end of the file pick the kernel.
 //
-// One MFMA mainloop serves all of them. The output tile is BR "P rows" x BC "Q columns"; P feeds
+// 16-bit operands with K a multiple of 64 run the eight-wave ring kernels of moe_gemm_v4.h
+// (token_gemm_v4_kernel, wgrad_v4_kernel below); row-contiguous weights with other K run the
+// five-stage kernel of moe_gemm_v3.h. The first-generation kernels described next serve fp32 and
+// the remaining 16-bit shapes.
+//
+// First generation: one MFMA mainloop. The output tile is BR "P rows" x BC "Q columns"; P feeds
 // the MFMA A side and is always the operand whose index is contiguous in the output, so each lane
 // ends up owning four consecutive output elements (one 8-byte bf16 store). Both operands are
 // staged through LDS as [row][128 bytes of K] with a 16-byte pad per row (conflict-free 16-byte

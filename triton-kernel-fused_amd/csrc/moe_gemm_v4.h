@@ -1,4 +1,4 @@
-// Grouped GEMM, fourth generation (16-bit operands, both K-contiguous): 256x256 output tile per
+// Grouped GEMM, fourth generation (16-bit and fp8 operands): 256x256 output tile per
 // workgroup of EIGHT waves, two per SIMD. Each wave owns a 128 (P) x 64 (Q) sub-tile: 8 x 4 MFMA
 // 16x16x32 tiles (token GEMMs) or 4 x 2 32x32x16 / 32x32x64-fp8 tiles (weight gradients, fp8),
 // 128 accumulators per lane either way, so two waves fit one SIMD's register file.
@@ -6,8 +6,8 @@
 // Why eight waves: with one wave per SIMD, every LDS-read wait and barrier of that wave idles its
 // SIMD's MFMA pipe; with two, the other wave's MFMAs fill the gap. Measured on the config-3 gate/up
 // GEMM with the loads switched off, the K loop runs at ~1.6-1.8 PFLOP/s against ~1.3-1.45 for the
-// four-wave 128x128-per-wave kernel. LDS read traffic grows 1.5x (6 fragment reads per 8 MFMAs
-// instead of 8 per 16), which gfx950's LDS (about 230 bytes per clock per CU for 16-byte reads)
+// four-wave 128x128-per-wave kernel. LDS read traffic per FLOP grows 1.5x (a 128x64 wave block
+// instead of 128x128), which gfx950's LDS (about 230 bytes per clock per CU for 16-byte reads)
 // absorbs.
 //
 // LDS row layout and K step are those of moe_gemm_v2.h: K steps of 64 16-bit values (one 128-byte
