@@ -249,3 +249,18 @@ def test_bf16_k_not_multiple_of_64(h, i):
     ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
     mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
     _assert_bf16(mine, ref)
+
+
+def test_bf16_out_of_range_expert_ids():
+    """Out-of-range expert ids (>= E and negative) are dropped, as the oracle's mask drops them:
+    their slots add nothing and their gate gradients are zero. Exercises the folded backward with
+    routed rows fewer than N*k (the gates gathered into sorted order past the routed count)."""
+    codes = [0, 1, 0, 1, 0, 0]
+    hid, idx, w, gu, dw, codes_t, ap, go = _case(codes, 6, dtype=torch.bfloat16, n=400, h=128,
+                                                 i=96, k=3, seed=7)
+    idx[::7, 0] = 6
+    idx[::11, 1] = -1
+    _say("bf16 out-of-range expert ids")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
+    mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
+    _assert_bf16(mine, ref)
