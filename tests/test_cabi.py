@@ -69,6 +69,12 @@ def test_gemm_entry_points_reject_bad_arguments():
     assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 64, None, 64, 64, fake, fake, 3, 4, fake, None) == 1
     assert h.moe_combine_fwd(2, fake, fake, fake, fake, fake, 4, 5, fake, 10, 2, 64, 0, fake, None) == 1
     assert h.moe_glu_fwd(2, fake, 10, fake, fake, None, 1, 4, 8, fake, 8, None) == 1
+    # gate-weighted intermediate: 16-bit only, H % 64 == 0, inter_out required
+    gu = [2, fake, 10, 64, fake, 4, 64, fake, fake, None, fake, 20, fake]
+    assert h.moe_grouped_gateup_swiglu_fwd(0, *gu[1:], fake, fake, None, None) == 1  # fp32
+    assert h.moe_grouped_gateup_swiglu_fwd(*gu, None, fake, None, None) == 1  # no inter_out
+    gu96 = [2, fake, 10, 96, fake, 4, 64, fake, fake, None, fake, 20, fake]
+    assert h.moe_grouped_gateup_swiglu_fwd(*gu96, fake, fake, None, None) == 1  # H % 64 != 0
 
 
 def test_call_maps_status_to_exceptions():
