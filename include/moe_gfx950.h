@@ -83,7 +83,15 @@ int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int64_t n_token
  * `it @ down_proj[e].t()` (:770) and torch._grouped_mm (kernels/sm120/moe_grouped.py:108). */
 int moe_grouped_down_fwd(int dtype, const void* inter, const void* down_proj, int E_glu, int64_t H,
                          int64_t I, const int32_t* offsets, const int32_t* tile_offsets,
-                         int64_t n_rows, void* eo_out, void* stream);
+                         int64_t n_rows, void* eo_out, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* Optional workspace of moe_grouped_down_fwd and moe_grouped_gateup_dx (no counterpart in the
+ * reference): bytes for the current device, 256-byte aligned, zero-filled once by the caller and
+ * left zero by every call; calls that share one workspace must be stream-ordered. With it, 16-bit
+ * GEMMs whose K spans at least 40 steps of 64 cut each XCD's last partial wave of tiles along K
+ * (partial tiles summed in a fixed order: results do not depend on timing). NULL: no split. */
+size_t moe_token_split_workspace_size(void);
 
 /* Gate-weighted combine: out[t] = sum_j w[t,j] * row(t,j), fp32 accumulation in slot order, where
  * row = eo[flat_to_sorted[t*k+j]] for GLU experts, hidden[t] for Identity (code 3), nothing for
@@ -122,7 +130,8 @@ int moe_grouped_down_dx_swiglu_bwd(int dtype, const void* grad_eo, const void* d
  * gate_up_proj[e]` (:822). */
 int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj, int E_glu, int64_t H,
                           int64_t I, const int32_t* offsets, const int32_t* tile_offsets,
-                          int64_t n_rows, void* grad_xs_out, void* stream);
+                          int64_t n_rows, void* grad_xs_out, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* Grouped weight gradient over each expert's ragged row range [offsets[e], offsets[e+1]):
  *   out[e, c, r] = sum_m  rsrc[rrow(m), r] * csrc[crow(m), c]

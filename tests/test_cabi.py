@@ -56,15 +56,15 @@ def test_gemm_entry_points_reject_bad_arguments():
     h = _lib.lib()
     fake = 256
     # dtype
-    assert h.moe_grouped_down_fwd(7, fake, fake, 4, 64, 64, fake, None, 10, fake, None) == 4
+    assert h.moe_grouped_down_fwd(7, fake, fake, 4, 64, 64, fake, None, 10, fake, None, 0, None) == 4
     # H not a multiple of 8
-    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 60, 64, fake, None, 10, fake, None) == 2
+    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 60, 64, fake, None, 10, fake, None, 0, None) == 2
     # misaligned pointer
-    assert h.moe_grouped_down_fwd(2, fake + 2, fake, 4, 64, 64, fake, None, 10, fake, None) == 2
+    assert h.moe_grouped_down_fwd(2, fake + 2, fake, 4, 64, 64, fake, None, 10, fake, None, 0, None) == 2
     # no experts
-    assert h.moe_grouped_down_fwd(2, fake, fake, 0, 64, 64, fake, None, 10, fake, None) == 1
+    assert h.moe_grouped_down_fwd(2, fake, fake, 0, 64, 64, fake, None, 10, fake, None, 0, None) == 1
     # zero rows is a no-op success
-    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 64, 64, fake, None, 0, fake, None) == 0
+    assert h.moe_grouped_down_fwd(2, fake, fake, 4, 64, 64, fake, None, 0, fake, None, 0, None) == 0
     assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, None, 4, 4, fake, None) == 2
     assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 64, None, 64, 64, fake, fake, 3, 4, fake, None) == 1
     assert h.moe_combine_fwd(2, fake, fake, fake, fake, fake, 4, 5, fake, 10, 2, 64, 0, fake, None) == 1
@@ -79,9 +79,9 @@ def test_gemm_entry_points_reject_bad_arguments():
 
 def test_call_maps_status_to_exceptions():
     with pytest.raises(TypeError):
-        _lib.call("moe_grouped_down_fwd", 9, 16, 16, 4, 64, 64, 16, None, 10, 16, None)
+        _lib.call("moe_grouped_down_fwd", 9, 16, 16, 4, 64, 64, 16, None, 10, 16, None, 0, None)
     with pytest.raises(ValueError):
-        _lib.call("moe_grouped_down_fwd", 2, 18, 16, 4, 64, 64, 16, None, 10, 16, None)
+        _lib.call("moe_grouped_down_fwd", 2, 18, 16, 4, 64, 64, 16, None, 10, 16, None, 0, None)
 
 
 def test_host_tensors_fail_loudly():

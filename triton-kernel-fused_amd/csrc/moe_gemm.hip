@@ -635,8 +635,39 @@ token_gemm_v4_kernel(TokenArgs a) {
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
-  int mt, rt;
-  if (!v4::block_tile(s_pref[a.E_glu], a.n_rtiles, mt, rt)) return;
+  // Block -> tile as v4::block_tile. With a split workspace (plain-store GEMMs, K of at least
+  // SPLIT_MIN_STEPS steps), each XCD's last partial wave -- rem tiles for its xcd_cus slots -- is
+  // cut along K into S pieces per tile, all on that XCD.
+  const int nk = a.K / 64;
+  int mt, rt, piece = 0, S = 1, slot0 = 0;
+  {
+    const int n_mt = s_pref[a.E_glu];
+    const int gm = v4::tile_group(a.n_rtiles);
+    const int n_idx = (n_mt + gm - 1) / gm * gm * a.n_rtiles;
+    const int x = (int)blockIdx.x & 7, bi = (int)blockIdx.x >> 3;
+    const int R = (n_idx + 7) >> 3;
+    const int t_lo = x * R, t_cnt = max(0, min(n_idx, t_lo + R) - t_lo);
+    const int cus = a.xcd_cus;
+    const bool split = EPI == EPI_STORE && a.split_ws && nk >= v4::SPLIT_MIN_STEPS;
+    const int full = split ? t_cnt / cus * cus : t_cnt;
+    const int rem = t_cnt - full;
+    S = rem > 0 ? min(min(cus / rem, nk / 8), v4::SPLIT_MAX) : 1;
+    int lid;
+    if (bi < full || S <= 1) {
+      if (bi >= t_cnt) return;
+      lid = t_lo + bi;
+      S = 1;
+    } else {
+      const int j = bi - full;
+      if (j >= rem * S) return;
+      lid = t_lo + full + j / S;
+      piece = j % S;
+      slot0 = x * cus + (j / S) * S;
+    }
+    v4::tile_of(lid, a.n_rtiles, mt, rt);
+    if (mt >= n_mt) return;
+  }
+  const int kb = piece * nk / S * 64, ke = (piece + 1) * nk / S * 64;
   int lo = 0, hi = a.E_glu - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -684,7 +715,7 @@ token_gemm_v4_kernel(TokenArgs a) {
     lp.kend = a.K;
     lp.init(wr * v4::WP, a.R - r0);
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
-    v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
+    v4::mainloop_ring<T>(acc, lp, lq, kb, ke, smem);
   } else {
     typename V4Sh16::Kc lp;
     lp.init(wr * v4::WP);
@@ -702,7 +733,38 @@ token_gemm_v4_kernel(TokenArgs a) {
       lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
     }
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
-    v4::mainloop_ring<T>(acc, lp, lq, 0, a.K, smem);
+    v4::mainloop_ring<T>(acc, lp, lq, kb, ke, smem);
+  }
+  if (S > 1) {
+    // Split piece: every piece stores its partial tile and, after a device-scope release, counts
+    // itself in; the last to arrive acquires, sums all pieces in piece order (the same result
+    // whichever arrives last), clears the counter and runs the epilogue. Nothing waits on another
+    // workgroup.
+    f32x4* ws = (f32x4*)a.split_ws;
+    constexpr int NV = V4Sh16::TI * V4Sh16::TJ;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      ws[((size_t)(slot0 + piece) * NV + v) * v4::NT + threadIdx.x] = acc[v / V4Sh16::TJ][v % V4Sh16::TJ];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    int* s_flag = (int*)smem;  // the ring is idle between the K loop and the epilogue
+    if (threadIdx.x == 0) {
+      const int old = __hip_atomic_fetch_add(a.split_cnt + slot0, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      if (old == S - 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      *s_flag = old;
+    }
+    __syncthreads();
+    const bool last = *s_flag == S - 1;
+    __syncthreads();  // every wave has read the flag before the epilogue reuses the LDS
+    if (!last) return;
+    V4Sh16::zero(acc);
+    for (int q = 0; q < S; ++q) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        acc[v / V4Sh16::TJ][v % V4Sh16::TJ] += ws[((size_t)(slot0 + q) * NV + v) * v4::NT + threadIdx.x];
+    }
+    if (threadIdx.x == 0) a.split_cnt[slot0] = 0;
   }
   float wrow = 1.f;
   if constexpr (WGATE) {
@@ -872,7 +934,8 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
   const int64_t logical = v4::logical_tiles(max_mt, a.n_rtiles);
   if (logical <= 0 || n_rows == 0) return MOE_OK;
-  const int64_t grid = (logical + 7) / 8 * 8;
+  int64_t grid = (logical + 7) / 8 * 8;
+  if (a.split_ws && a.K % 64 == 0) grid += 8 * (int64_t)a.xcd_cus;  // the split pieces
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
   if (a.K % 64 == 0) {
     auto kern = token_gemm_v4_kernel<T, EPI, P_RC>;
@@ -984,10 +1047,36 @@ extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int6
   }
 }
 
+// Workgroup slots of the current device (CUs; one 160 KB-LDS workgroup each).
+static int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
+extern "C" size_t moe_token_split_workspace_size(void) {
+  const int n = device_cus();
+  if (n <= 0) return 0;
+  return (size_t)n * 65536 * sizeof(float) + (((size_t)n * sizeof(int) + 255) & ~(size_t)255);
+}
+
+// Attach a caller's split workspace (NULL: none). MOE_OK or MOE_ERR_WORKSPACE.
+static int attach_split(TokenArgs& a, void* workspace, size_t workspace_bytes) {
+  if (!workspace) return MOE_OK;
+  const int n = device_cus();
+  if (n < 8 || workspace_bytes < moe_token_split_workspace_size() || ((uintptr_t)workspace & 255))
+    return MOE_ERR_WORKSPACE;
+  a.split_ws = (float*)workspace;
+  a.split_cnt = (int*)((char*)workspace + (size_t)n * 65536 * sizeof(float));
+  a.xcd_cus = n / 8;
+  return MOE_OK;
+}
+
 extern "C" int moe_grouped_down_fwd(int dtype, const void* inter, const void* down_proj, int E_glu,
                                     int64_t H, int64_t I, const int32_t* offsets,
                                     const int32_t* tile_offsets, int64_t n_rows, void* eo_out,
-                                    void* stream) {
+                                    void* workspace, size_t workspace_bytes, void* stream) {
   (void)tile_offsets;
   int st = check_common(dtype, H, I, E_glu, n_rows);
   if (st) return st;
@@ -999,6 +1088,7 @@ extern "C" int moe_grouped_down_fwd(int dtype, const void* inter, const void* do
   a.Q = inter; a.q_ld = I; a.q_gather = nullptr;
   a.offsets = offsets; a.E_glu = E_glu; a.I = (int)I;
   a.out = eo_out; a.out_ld = H;
+  if ((st = attach_split(a, workspace, workspace_bytes))) return st;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {
@@ -1089,7 +1179,8 @@ extern "C" int moe_grouped_down_dx_gated_bwd(int dtype, const void* grad_out, in
 extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj,
                                      int E_glu, int64_t H, int64_t I, const int32_t* offsets,
                                      const int32_t* tile_offsets, int64_t n_rows,
-                                     void* grad_xs_out, void* stream) {
+                                     void* grad_xs_out, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
   (void)tile_offsets;
   int st = check_common(dtype, H, I, E_glu, n_rows);
   if (st) return st;
@@ -1102,6 +1193,7 @@ extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gat
   a.Q = ggu; a.q_ld = 2 * I; a.q_gather = nullptr;
   a.offsets = offsets; a.E_glu = E_glu; a.I = (int)I;
   a.out = grad_xs_out; a.out_ld = H;
+  if ((st = attach_split(a, workspace, workspace_bytes))) return st;
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {

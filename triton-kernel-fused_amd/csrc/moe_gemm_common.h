@@ -109,6 +109,12 @@ struct TokenArgs {
   const int32_t* sflat;    // sorted row -> flat slot t*k+j
   float* part;             // gate-gradient partials (2 * n_rtiles, M): sum over a wave's 128
                            // channels of (grad_out @ down_proj) * inter
+  // K-split of each XCD's last partial wave (v4 kernel, EPI_STORE; null split_ws = off): fp32
+  // partial tiles, one per workgroup slot (xcd_cus per XCD), then per-tile arrival counters (zero
+  // on entry, left zero).
+  float* split_ws;
+  int* split_cnt;
+  int xcd_cus;
 };
 
 // Block-wide exclusive scan of the per-expert tile counts into s_pref[0..E]; returns the total.

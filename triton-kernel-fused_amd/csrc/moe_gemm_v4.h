@@ -36,6 +36,12 @@ constexpr int TI16 = WP / 16;    // 8   (16x16x32 MFMA tiles: 16-bit operands)
 constexpr int TJ16 = WQ / 16;    // 4
 constexpr int OPB = TILE * ROWB; // 32 KB: one operand's K step
 constexpr int LOADS = TILE / NW / 8;  // DMA instructions per wave per operand per step (4)
+// K-split of the last partial wave: only for K of at least SPLIT_MIN_STEPS ring steps (the
+// handoff's device-scope acquire invalidates the XCD's L2, which costs short-K GEMMs more than
+// the split saves: measured +20% on a 88-step dX GEMM, -2 to -8% at 16-32 steps), at most
+// SPLIT_MAX pieces of at least 8 steps.
+constexpr int SPLIT_MIN_STEPS = 40;
+constexpr int SPLIT_MAX = 4;
 
 __device__ __forceinline__ int lane_id() { return (int)threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); }

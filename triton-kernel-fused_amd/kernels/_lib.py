@@ -26,10 +26,11 @@ _SIGS = {
     "moe_version": [],
     "moe_tile_rows": [],
     "moe_get_workspace_size": [_L, _I, _I],
+    "moe_token_split_workspace_size": [],
     "moe_dispatch": [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
     "moe_grouped_gateup_swiglu_fwd": [_I, _P, _L, _L, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P, _P,
                                       _P, _P],
-    "moe_grouped_down_fwd": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
+    "moe_grouped_down_fwd": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P, _S, _P],
     "moe_combine_fwd": [_I, _P, _P, _P, _P, _P, _I, _I, _P, _L, _I, _L, _I, _P, _P],
     "moe_combine_bwd": [_I, _P, _L, _P, _P, _P, _P, _P, _I, _I, _P, _P, _L, _I, _L, _P, _P, _P],
     "moe_grouped_down_dx_swiglu_bwd": [_I, _P, _P, _I, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P],
@@ -37,7 +38,7 @@ _SIGS = {
                                       _P, _P, _P, _P],
     "moe_gate_grad_parts": [_L],
     "moe_gate_grad": [_I, _P, _I, _L, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
-    "moe_grouped_gateup_dx": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P],
+    "moe_grouped_gateup_dx": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P, _S, _P],
     "moe_grouped_wgrad": [_I, _P, _L, _P, _P, _L, _P, _L, _L, _P, _P, _I, _I, _P, _P],
     "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_glu_fwd": [_I, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P],
@@ -49,7 +50,8 @@ _SIGS = {
     "moe_router_bias_update": [_P, _P, _I, _F, _P],
     "moe_mxfp8_fwd": [_P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P],
 }
-_RESTYPES = {"moe_version": ctypes.c_char_p, "moe_gate_grad_parts": ctypes.c_int, "moe_get_workspace_size": ctypes.c_size_t}
+_RESTYPES = {"moe_version": ctypes.c_char_p, "moe_gate_grad_parts": ctypes.c_int, "moe_get_workspace_size": ctypes.c_size_t,
+             "moe_token_split_workspace_size": ctypes.c_size_t}
 
 _ERRORS = {
     1: (ValueError, "shape"),
@@ -111,6 +113,23 @@ def call(name, *args, tag=None):
 def ptr(t):
     """Device pointer of a tensor (None -> NULL)."""
     return None if t is None else t.data_ptr()
+
+
+_SPLIT_WS = {}
+
+
+def split_workspace(device):
+    """The token GEMMs' split workspace for `device` and its current stream: zero-filled once and
+    kept zero by the kernels; one per stream, since calls that share one must be stream-ordered.
+    Returns (pointer, bytes)."""
+    key = (torch.device(device).index, stream_of(device))
+    ws = _SPLIT_WS.get(key)
+    if ws is None:
+        n = lib().moe_token_split_workspace_size()
+        if n == 0:
+            return None, 0
+        ws = _SPLIT_WS[key] = torch.zeros(n, device=device, dtype=torch.uint8)
+    return ws.data_ptr(), ws.numel()
 
 
 def stream_of(device):

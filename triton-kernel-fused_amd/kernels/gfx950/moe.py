@@ -204,7 +204,7 @@ class _MoEFunction(torch.autograd.Function):
                           stream)
             _lib.call("moe_grouped_down_fwd", dtc, _lib.ptr(inter), _lib.ptr(down_proj), e_glu, h,
                       inter_dim, _lib.ptr(routing.offsets), _lib.ptr(routing.tile_offsets), m,
-                      _lib.ptr(eo), stream)
+                      _lib.ptr(eo), *_lib.split_workspace(dev), stream)
         out = torch.empty(n_tok, h, device=dev, dtype=dt)
         _lib.call("moe_combine_fwd", dtc, _lib.ptr(eo), _lib.ptr(hidden), _lib.ptr(wt),
                   _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu, _lib.ptr(routing.flat_to_sorted),
@@ -308,7 +308,8 @@ class _MoEFunction(torch.autograd.Function):
                 gxs = torch.empty(m, h, device=dev, dtype=dt)
                 _lib.call("moe_grouped_gateup_dx", dtc, _lib.ptr(ggu), _lib.ptr(gate_up_proj),
                           e_glu, h, inter_dim, _lib.ptr(routing.offsets),
-                          _lib.ptr(routing.tile_offsets), m, _lib.ptr(gxs), stream)
+                          _lib.ptr(routing.tile_offsets), m, _lib.ptr(gxs),
+                          *_lib.split_workspace(dev), stream)
             g_x = torch.empty(n_tok, h, device=dev, dtype=dt)
             _lib.call("moe_unpermute_bwd", dtc, _lib.ptr(gxs), _lib.ptr(go), go_ld, _lib.ptr(wt),
                       _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu if gxs is not None else 0,
@@ -364,7 +365,7 @@ def _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap):
         gxs = torch.empty(m, h, device=dev, dtype=dt)
         _lib.call("moe_grouped_gateup_dx", dtc, _lib.ptr(ggu), _lib.ptr(gate_up_proj), e_glu, h,
                   inter_dim, _lib.ptr(routing.offsets), _lib.ptr(routing.tile_offsets), m,
-                  _lib.ptr(gxs), stream)
+                  _lib.ptr(gxs), *_lib.split_workspace(dev), stream)
         g_x = torch.empty(n_tok, h, device=dev, dtype=dt)
         _lib.call("moe_unpermute_bwd", dtc, _lib.ptr(gxs), _lib.ptr(go), go_ld, _lib.ptr(wt),
                   _lib.ptr(idx), _lib.ptr(codes_t), n_exp, e_glu, _lib.ptr(routing.flat_to_sorted),
