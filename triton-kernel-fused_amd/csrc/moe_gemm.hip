@@ -678,6 +678,8 @@ token_gemm_v4_kernel(TokenArgs a) {
   const int m_end = a.offsets[e + 1];
   const T* Pe = (const T*)a.P + (size_t)e * a.p_e;
   const int wr = v4::wave_r(), wc = v4::wave_c();
+  // Waves whose 64 token rows all lie past the group end (tail tiles) skip their MFMAs.
+  const bool wave_rows = m0 + wc * v4::WQ < m_end;
 
   // Gate of this lane's token row (gated backward; weighted forward intermediate), needed only by
   // the epilogue, loaded with the token-row indices below. sflat null: the gates are already in
@@ -715,7 +717,8 @@ token_gemm_v4_kernel(TokenArgs a) {
     lp.kend = a.K;
     lp.init(wr * v4::WP, a.R - r0);
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
-    v4::mainloop_ring<T>(acc, lp, lq, kb, ke, smem);
+    if (wave_rows) v4::mainloop_ring<T, true>(acc, lp, lq, kb, ke, smem);
+    else v4::mainloop_ring<T, false>(acc, lp, lq, kb, ke, smem);
   } else {
     typename V4Sh16::Kc lp;
     lp.init(wr * v4::WP);
@@ -733,7 +736,8 @@ token_gemm_v4_kernel(TokenArgs a) {
       lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
     }
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
-    v4::mainloop_ring<T>(acc, lp, lq, kb, ke, smem);
+    if (wave_rows) v4::mainloop_ring<T, true>(acc, lp, lq, kb, ke, smem);
+    else v4::mainloop_ring<T, false>(acc, lp, lq, kb, ke, smem);
   }
   if (S > 1) {
     // Split piece: every piece stores its partial tile and, after a device-scope release, counts

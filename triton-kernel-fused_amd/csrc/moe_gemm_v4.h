@@ -230,7 +230,9 @@ __device__ __forceinline__ void wait_slots(int n) {
 // than issuing them in bursts. Refills past the end re-read the last K step into slots nobody
 // reads again, and the prologue fills the slots the same way at every K length, so every wait is
 // a constant; the loop end waits for all DMAs.
-template <typename T, typename AccV, int TI_, int TJ_, class LP, class LQ>
+// COMPUTE false (a wave whose token rows are all past the group end): the same loads, LDS reads
+// and barriers, no MFMAs, so the SIMD's other wave has the matrix pipe to itself.
+template <typename T, bool COMPUTE = true, typename AccV, int TI_, int TJ_, class LP, class LQ>
 __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ& lq, int k0, int k1,
                                               char* smem) {
   constexpr int KS = v2::bk<T>();
@@ -322,7 +324,7 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
         __builtin_amdgcn_sched_barrier(0);
         static_for<0, NM>([&](auto ic) {
           constexpr int I = decltype(ic)::value;
-          Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
+          if constexpr (COMPUTE) Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
           __builtin_amdgcn_sched_barrier(0);
           if constexpr (I < TJ_) {
 #pragma unroll
