@@ -83,7 +83,9 @@ fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
   __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
-  v4::mainloop_ring<fp8e4m3>(acc, lp, lq, 0, a.K, smem);
+  // Waves whose 64 token rows all lie past the group end (tail tiles) skip their MFMAs.
+  if (m0 + wc * v4::WQ < m_end) v4::mainloop_ring<fp8e4m3, true>(acc, lp, lq, 0, a.K, smem);
+  else v4::mainloop_ring<fp8e4m3, false>(acc, lp, lq, 0, a.K, smem);
 
   // Epilogue: scales applied in fp32 in registers, then the bf16 results of each wave are staged
   // in its own LDS block (the ring's final barrier has released the LDS) and stored as whole row
