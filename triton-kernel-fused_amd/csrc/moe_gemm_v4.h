@@ -230,8 +230,9 @@ __device__ __forceinline__ void wait_slots(int n) {
 // than issuing them in bursts. Refills past the end re-read the last K step into slots nobody
 // reads again, and the prologue fills the slots the same way at every K length, so every wait is
 // a constant; the loop end waits for all DMAs.
-// COMPUTE false (a wave whose token rows are all past the group end): the same loads, LDS reads
-// and barriers, no MFMAs, so the SIMD's other wave has the matrix pipe to itself.
+// COMPUTE false (a wave whose token rows are all past the group end): the same loads and
+// barriers, no fragment reads and no MFMAs, so the SIMD's other wave has the LDS and the matrix
+// pipe to itself.
 template <typename T, bool COMPUTE = true, typename AccV, int TI_, int TJ_, class LP, class LQ>
 __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ& lq, int k0, int k1,
                                               char* smem) {
@@ -326,12 +327,12 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
           constexpr int I = decltype(ic)::value;
           if constexpr (COMPUTE) Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (I < TJ_) {
+          if constexpr (COMPUTE && I < TJ_) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) rb[f ^ 1][I][c] = lq.template frag<CPL>(nqs, I, nsl, c);
           }
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (I % TJ_ == TJ_ - 1) {
+          if constexpr (COMPUTE && I % TJ_ == TJ_ - 1) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) ra[I / TJ_][c] = lp.template frag<CPL>(nps, I / TJ_, nsl, c);
           }
