@@ -446,6 +446,7 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
   const int row0 = m0 + wc * WQ;
   v2::stage_acc<T>(acc, wl);
   __syncthreads();
+  if (row0 >= m_end) return;  // this wave's token rows all lie past the group end
   if constexpr (EPI == EPI_STORE) {
     v2::store_staged<T, WQ>(wl, (T*)a.out, a.out_ld, row0, m_end, rt * v2::TILE + wr * v2::WT, a.R);
   } else if constexpr (EPI == EPI_GLU_FWD) {
