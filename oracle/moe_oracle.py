@@ -206,58 +206,60 @@ FP8_MAX = 448.0
 
 def e4m3_round(x):
     """Round fp32 to the nearest e4m3fn value (saturating at +-448)."""
-    return x.clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn).float()
+    return x.clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn).to(x.dtype)
 
 
 def fp8_forward(x_q, x_scale, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale,
-                requant_inter=True, inter_bf16=False):
+                requant_inter=True, inter_bf16=False, dtype=torch.float32):
     """fp8 MoE forward in fp32 from quantised operands.
     gate_up = (x_q . W_q^T) * x_scale[t] * w_scale[n]; inter = SiLU(gate)*up (rounded to bf16 first
     when inter_bf16, as a kernel that stores it in bf16 does), re-quantised per row (absmax/448)
     when requant_inter; eo = (inter_q . Wd_q^T) * inter_scale * wd_scale[h];
-    out[t] = sum_j w[t,j] * eo (fp32). Returns fp32 (N,H)."""
+    out[t] = sum_j w[t,j] * eo, all in `dtype` (fp32 by default). Returns (N,H) in `dtype`."""
     n, h = x_q.shape
     inter = gate_up_q.shape[1] // 2
-    xf = x_q.float()
-    out = torch.zeros(n, h, device=x_q.device)
+    xf = x_q.to(dtype)
+    xs = x_scale.to(dtype)
+    out = torch.zeros(n, h, device=x_q.device, dtype=dtype)
     for e in range(gate_up_q.shape[0]):
         hit = idx == e
         rows = hit.any(-1)
         if not bool(rows.any()):
             continue
-        w = (wt.float() * hit).sum(-1)[rows].unsqueeze(-1)
-        gu = (xf[rows] @ gate_up_q[e].float().T) * x_scale[rows].unsqueeze(-1) * gate_up_scale[e]
+        w = (wt.to(dtype) * hit).sum(-1)[rows].unsqueeze(-1)
+        gu = (xf[rows] @ gate_up_q[e].to(dtype).T) * xs[rows].unsqueeze(-1) * gate_up_scale[e].to(dtype)
         y = F.silu(gu[:, :inter]) * gu[:, inter:]
         if inter_bf16:
-            y = y.bfloat16().float()
+            y = y.bfloat16().to(dtype)
         if requant_inter:
             amax = y.abs().amax(-1, keepdim=True)
             s = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
             y = e4m3_round(y / s) * s
-        eo = (y @ down_q[e].float().T) * down_scale[e]
+        eo = (y @ down_q[e].to(dtype).T) * down_scale[e].to(dtype)
         out[rows] += eo * w
     return out
 
 
-def mxfp8_forward(hidden, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale):
+def mxfp8_forward(hidden, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale,
+                  dtype=torch.float32):
     """MXFP8-weight MoE forward: weights dequantised per expert (E8M0 block scales along K),
-    activations as given (bf16 values), fp32 math. Returns fp32 (N,H)."""
+    activations as given (bf16 values), math in `dtype` (fp32 by default). Returns (N,H)."""
     n, h = hidden.shape
     inter = gate_up_q.shape[1] // 2
-    x = hidden.float()
-    out = torch.zeros(n, h, device=hidden.device)
+    x = hidden.to(dtype)
+    out = torch.zeros(n, h, device=hidden.device, dtype=dtype)
 
     def deq(q, s):
         k = q.shape[-1]
-        return (q.float().reshape(q.shape[0], k // 32, 32) *
-                torch.exp2(s.float() - 127.0).unsqueeze(-1)).reshape(q.shape[0], k)
+        return (q.to(dtype).reshape(q.shape[0], k // 32, 32) *
+                torch.exp2(s.to(dtype) - 127.0).unsqueeze(-1)).reshape(q.shape[0], k)
 
     for e in range(gate_up_q.shape[0]):
         hit = idx == e
         rows = hit.any(-1)
         if not bool(rows.any()):
             continue
-        w = (wt.float() * hit).sum(-1)[rows].unsqueeze(-1)
+        w = (wt.to(dtype) * hit).sum(-1)[rows].unsqueeze(-1)
         gu = x[rows] @ deq(gate_up_q[e], gate_up_scale[e]).T
         y = F.silu(gu[:, :inter]) * gu[:, inter:]
         out[rows] += (y @ deq(down_q[e], down_scale[e]).T) * w

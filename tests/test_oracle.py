@@ -10,6 +10,7 @@ function is pinned by something that does not share its formula:
   fp8 / MXFP8     quantiser round trips, exact powers of two, and error bounds;
   fixture         vs tests/golden/config1.npz (regression of generator + oracle).
 """
+import math
 import os
 
 import numpy as np
@@ -182,6 +183,121 @@ def test_fp8_forward_requant_only_differs_by_intermediate():
     b = orc.fp8_forward(*args, requant_inter=False)
     rel = ((a - b).norm() / b.norm()).item()
     assert 1e-4 < rel < 5e-2
+
+
+# ── independent pins of the fp8 / MXFP8 forwards ──
+# The reference has no quantised path, so these pins come from the mathematics: (1) without the
+# intermediate re-quantisation, the fp8 forward is the plain MoE forward on dequantised operands
+# (the scales factor out of every dot product); (2) the MXFP8 forward is the plain MoE forward on
+# block-dequantised weights; (3) the whole fp8 pipeline, re-quantisation included, equals scalar
+# Python loops whose e4m3 rounding is a nearest-value search over the 8-bit code table decoded
+# from its bit fields (no torch float8 conversion involved).
+
+def _e4m3_table():
+    """All finite non-negative e4m3fn values from their bit fields: (value, code) pairs."""
+    out = []
+    for code in range(0x7F):                       # 0x7F is NaN; the sign bit is handled apart
+        e, m = code >> 3, code & 7
+        v = (m / 8.0) * 2.0 ** -6 if e == 0 else (1.0 + m / 8.0) * 2.0 ** (e - 7)
+        out.append((v, code))
+    return out
+
+
+_E4M3 = _e4m3_table()
+
+
+def _e4m3_round_loop(x):
+    """Nearest e4m3fn value by exhaustive search, ties to the even code, saturating at 448."""
+    a = min(abs(x), 448.0)
+    best = min(_E4M3, key=lambda vc: (abs(vc[0] - a), vc[1] & 1))
+    return best[0] if x >= 0 else -best[0]
+
+
+def test_e4m3_table_is_the_format():
+    vals = [v for v, _ in _E4M3]
+    assert vals[1] == 2.0 ** -9 and vals[8] == 2.0 ** -6 and vals[-1] == 448.0
+    assert len(set(vals)) == 127 and vals == sorted(vals)
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(400, generator=g, dtype=torch.float64) * torch.logspace(-4, 3, 400,
+                                                                            dtype=torch.float64))
+    x = torch.cat([x, torch.tensor([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 500.0, -1e9],
+                                   dtype=torch.float64)])
+    ref = torch.tensor([_e4m3_round_loop(float(v)) for v in x], dtype=torch.float64)
+    assert torch.equal(orc.e4m3_round(x), ref)
+
+
+def _tiny_fp8_case(seed=0):
+    return make_workload(4, seed=seed, scale=dict(N=6, H=32, I=32, E=3, k=2))
+
+
+def test_fp8_forward_without_requant_is_moe_forward_on_dequantised_operands():
+    w = make_workload(4, scale=dict(N=48, H=64, I=64, E=5, k=3), seed=2)
+    f64 = torch.float64
+    got = orc.fp8_forward(w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"],
+                          w["gate_up_scale"], w["down_q"], w["down_scale"], requant_inter=False,
+                          dtype=f64)
+    x = w["x_q"].to(f64) * w["x_scale"].to(f64).unsqueeze(-1)
+    gu = w["gate_up_q"].to(f64) * w["gate_up_scale"].to(f64).unsqueeze(-1)
+    dw = w["down_q"].to(f64) * w["down_scale"].to(f64).unsqueeze(-1)
+    ref = orc.moe_dense(x, w["idx"], w["wt"].to(f64), gu, dw, [0] * 5)
+    torch.testing.assert_close(got, ref, rtol=1e-10, atol=1e-10)
+    ref2 = orc.moe_forward(x, w["idx"], w["wt"].to(f64), gu, dw, [0] * 5)
+    torch.testing.assert_close(got, ref2, rtol=1e-10, atol=1e-10)
+
+
+def test_fp8_forward_with_requant_matches_scalar_loops():
+    w = _tiny_fp8_case(seed=3)
+    got = orc.fp8_forward(w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"],
+                          w["gate_up_scale"], w["down_q"], w["down_scale"], requant_inter=True,
+                          dtype=torch.float64)
+    xq, xs = w["x_q"].double().tolist(), w["x_scale"].double().tolist()
+    gq, gs = w["gate_up_q"].double().tolist(), w["gate_up_scale"].double().tolist()
+    dq, ds = w["down_q"].double().tolist(), w["down_scale"].double().tolist()
+    idx, wt = w["idx"].tolist(), w["wt"].double().tolist()
+    n, h, i = 6, 32, 32
+    ref = [[0.0] * h for _ in range(n)]
+    for t in range(n):
+        for j, e in enumerate(idx[t]):
+            gu = [sum(xq[t][c] * gq[e][r][c] for c in range(h)) * xs[t] * gs[e][r]
+                  for r in range(2 * i)]
+            y = [gu[c] / (1.0 + math.exp(-gu[c])) * gu[i + c] for c in range(i)]
+            amax = max(abs(v) for v in y)
+            s = amax / 448.0 if amax > 0 else 1.0
+            y = [_e4m3_round_loop(v / s) * s for v in y]
+            for r in range(h):
+                ref[t][r] += wt[t][j] * sum(y[c] * dq[e][r][c] for c in range(i)) * ds[e][r]
+    torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=1e-9, atol=1e-9)
+
+
+def test_e8m0_block_dequantisation_loops():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 96, generator=g) * torch.tensor([[1e-3], [1.0], [40.0]])
+    q, s = quant.quantize_mxfp8(x)
+    qs, ss = q.float().tolist(), s.tolist()
+    ref = [[qs[r][c] * 2.0 ** (ss[r][c // 32] - 127) for c in range(96)] for r in range(3)]
+    assert torch.equal(quant.dequantize_mxfp8(q, s).double(), torch.tensor(ref, dtype=torch.float64))
+
+
+def test_mxfp8_forward_is_moe_forward_on_dequantised_weights():
+    w = make_workload(5, scale=dict(N=24, H=64, I=64, E=9, k=3), seed=1)
+    f64 = torch.float64
+    got = orc.mxfp8_forward(w["hidden"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"],
+                            w["down_q"], w["down_scale"], dtype=f64)
+    # weights dequantised by explicit loops over the E8M0 blocks
+    def deq(q, s):
+        qs, ss = q.double(), s.double()
+        out = torch.empty_like(qs)
+        for b in range(q.shape[-1] // 32):
+            out[..., 32 * b:32 * b + 32] = qs[..., 32 * b:32 * b + 32] * (2.0 ** (ss[..., b:b + 1] - 127))
+        return out
+    ref = orc.moe_dense(w["hidden"].to(f64), w["idx"], w["wt"].to(f64),
+                        deq(w["gate_up_q"], w["gate_up_scale"]), deq(w["down_q"], w["down_scale"]),
+                        [0] * 9)
+    torch.testing.assert_close(got, ref, rtol=1e-10, atol=1e-10)
+    # and the fp32 default agrees with the fp64 pin to fp32 accuracy
+    got32 = orc.mxfp8_forward(w["hidden"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"],
+                              w["down_q"], w["down_scale"])
+    assert ((got32.double() - ref).norm() / ref.norm()).item() < 1e-6
 
 
 def test_golden_config1():
