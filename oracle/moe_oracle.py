@@ -106,7 +106,9 @@ def moe_forward(hidden, idx, wt, gate_up_proj, down_proj, codes, act_params=None
     """fp32 (input dtype) eager MoE on the CPU. codes: list/tuple of ints."""
     n, h = hidden.shape
     inter = gate_up_proj.shape[1] // 2
-    out = torch.zeros(n, h, dtype=hidden.dtype, device=hidden.device)
+    # fp32 (or wider) accumulation, cast to the input dtype at the end (moe.py:893,909)
+    acc = torch.promote_types(hidden.dtype, torch.float32)
+    out = torch.zeros(n, h, dtype=acc, device=hidden.device)
     for e, code in enumerate(codes):
         hit = idx == e
         rows = hit.any(-1)
@@ -115,13 +117,13 @@ def moe_forward(hidden, idx, wt, gate_up_proj, down_proj, codes, act_params=None
         w = (wt * hit).sum(-1)[rows].unsqueeze(-1)
         x = hidden[rows]
         if code == 3:
-            out[rows] += x * w
+            out[rows] += (x * w).to(acc)
             continue
         gu = F.linear(x, gate_up_proj[e])
         a, g = (act_params[e, 0], act_params[e, 1]) if (code == 5 and act_params is not None) else (1.0, 1.0)
         y = act(gu[:, :inter], code, a, g) * gu[:, inter:]
-        out[rows] += F.linear(y, down_proj[e]) * w
-    return out
+        out[rows] += (F.linear(y, down_proj[e]) * w).to(acc)
+    return out.to(hidden.dtype)
 
 
 def moe_fwd_bwd(hidden, idx, wt, gate_up_proj, down_proj, codes, grad_out, act_params=None,

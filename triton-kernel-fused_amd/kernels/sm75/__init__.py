@@ -1,4 +1,8 @@
-"""Import-path alias: `from kernels.sm75 import moe` resolves to the gfx950 implementation."""
-from ..gfx950 import moe, moe_per_expert, moe_eager  # noqa: F401
+"""Import-path alias: `from kernels.sm75 import moe` resolves to the gfx950 implementation.
+The MoE and router names of the reference package (kernels/sm75/__init__.py:12-13) are bound from
+the submodules, so importing `kernels.sm75.moe` later does not rebind `kernels.sm75.moe`."""
+from .router import fused_router, router_bias_update, FusedConvRouterCuDNN  # noqa: F401
+from .moe import moe, moe_per_expert, moe_eager  # noqa: F401
 
-__all__ = ["moe", "moe_per_expert", "moe_eager"]
+__all__ = ["fused_router", "router_bias_update", "FusedConvRouterCuDNN",
+           "moe", "moe_per_expert", "moe_eager"]
