@@ -59,6 +59,18 @@ int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int 
                  int32_t* sorted_token, int32_t* sorted_flat, int32_t* flat_to_sorted,
                  int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free moe_dispatch: no counterpart in the reference. For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops): same arguments,
+ * outputs and results as moe_dispatch, minus the workspace, which is a 4 MiB file-scope device
+ * array per GPU instead (held until the process ends). Limit: ceil(N*k / 1024) * E <= 2^20
+ * (moe_get_workspace_size(...) <= 4 MiB; e.g. E = 64: N*k <= 16M rows), else MOE_ERR_WORKSPACE
+ * and nothing is launched. Every call on one GPU shares that array: calls that overlap on one GPU
+ * (different streams without ordering) race. Nothing in the array needs clearing between calls. */
+int moe_dispatch_noalloc(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int n_experts,
+                         int32_t* counts, int32_t* offsets, int32_t* tile_offsets,
+                         int32_t* expert_order, int32_t* sorted_token, int32_t* sorted_flat,
+                         int32_t* flat_to_sorted, int32_t* status, void* stream);
+
 /* Grouped gate/up projection with the GLU epilogue.
  * gate_up[m] = hidden[sorted_token[m]] @ gate_up_proj[e]^T for every sorted row m of a GLU expert
  * e < E_glu; inter[m, i] = act_e(gate) * up (act code 0 = SiLU, 1 = ReLU^2; the two codes the

@@ -11,6 +11,9 @@
 //                     of a row among equal experts comes from a ballot match (one ballot per id
 //                     bit) and a popcount; waves of one step are ordered through LDS counters.
 // A batch that fits one chunk runs all three passes in one workgroup (dispatch_small_kernel).
+#include <mutex>
+#include <unordered_map>
+
 #include "moe_common.h"
 
 namespace moe {
@@ -327,21 +330,13 @@ extern "C" size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_expe
   return (bytes + 255) & ~(size_t)255;
 }
 
-extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
-                            int n_experts, int32_t* counts, int32_t* offsets,
-                            int32_t* tile_offsets, int32_t* expert_order, int32_t* sorted_token,
-                            int32_t* sorted_flat, int32_t* flat_to_sorted, int32_t* status,
-                            void* workspace, size_t workspace_bytes, void* stream) {
-  if (n_tokens < 0 || top_k <= 0 || n_experts <= 0 || n_experts > MAX_EXPERTS) return MOE_ERR_SHAPE;
-  const int64_t M = n_tokens * top_k;
-  if (M >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  if (!counts || !offsets || !tile_offsets || !expert_order || !status) return MOE_ERR_SHAPE;
-  if (M > 0 && (!top_k_indices || !sorted_token || !sorted_flat || !flat_to_sorted))
-    return MOE_ERR_SHAPE;
-  if (!workspace || workspace_bytes < moe_get_workspace_size(n_tokens, top_k, n_experts))
-    return MOE_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  int32_t* hist = (int32_t*)workspace;
+// The three passes on a given histogram buffer (nchunks * E int32, fully written by the
+// histogram pass, so it needs no clearing).
+static int dispatch_launch(const int64_t* top_k_indices, int64_t M, int top_k, int n_experts,
+                           int32_t* counts, int32_t* offsets, int32_t* tile_offsets,
+                           int32_t* expert_order, int32_t* sorted_token, int32_t* sorted_flat,
+                           int32_t* flat_to_sorted, int32_t* status, int32_t* hist,
+                           hipStream_t s) {
   const int nc = (int)n_chunks(M);
   if (nc <= 1) {
     hipLaunchKernelGGL(dispatch_small_kernel, dim3(1), dim3(SMALL_THREADS), 0, s, top_k_indices, M,
@@ -349,16 +344,81 @@ extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int 
                        sorted_flat, flat_to_sorted, status);
     return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
   }
-  if (nc > 0) {
-    hipLaunchKernelGGL(dispatch_hist_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s, top_k_indices,
-                       M, n_experts, hist, status);
-  }
+  hipLaunchKernelGGL(dispatch_hist_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s, top_k_indices,
+                     M, n_experts, hist, status);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, s, hist, nc, n_experts, counts,
                      offsets, tile_offsets, expert_order);
-  if (nc > 0) {
-    hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s,
-                       top_k_indices, M, top_k, n_experts, hist, offsets, sorted_token,
-                       sorted_flat, flat_to_sorted);
-  }
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nc), dim3(DISPATCH_THREADS), 0, s,
+                     top_k_indices, M, top_k, n_experts, hist, offsets, sorted_token,
+                     sorted_flat, flat_to_sorted);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+}
+
+static int dispatch_check(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
+                          int n_experts, const int32_t* counts, const int32_t* offsets,
+                          const int32_t* tile_offsets, const int32_t* expert_order,
+                          const int32_t* sorted_token, const int32_t* sorted_flat,
+                          const int32_t* flat_to_sorted, const int32_t* status) {
+  if (n_tokens < 0 || top_k <= 0 || n_experts <= 0 || n_experts > MAX_EXPERTS) return MOE_ERR_SHAPE;
+  const int64_t M = n_tokens * top_k;
+  if (M >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  if (!counts || !offsets || !tile_offsets || !expert_order || !status) return MOE_ERR_SHAPE;
+  if (M > 0 && (!top_k_indices || !sorted_token || !sorted_flat || !flat_to_sorted))
+    return MOE_ERR_SHAPE;
+  return MOE_OK;
+}
+
+extern "C" int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
+                            int n_experts, int32_t* counts, int32_t* offsets,
+                            int32_t* tile_offsets, int32_t* expert_order, int32_t* sorted_token,
+                            int32_t* sorted_flat, int32_t* flat_to_sorted, int32_t* status,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  int st = dispatch_check(top_k_indices, n_tokens, top_k, n_experts, counts, offsets, tile_offsets,
+                          expert_order, sorted_token, sorted_flat, flat_to_sorted, status);
+  if (st) return st;
+  if (!workspace || workspace_bytes < moe_get_workspace_size(n_tokens, top_k, n_experts))
+    return MOE_ERR_WORKSPACE;
+  return dispatch_launch(top_k_indices, n_tokens * top_k, top_k, n_experts, counts, offsets,
+                         tile_offsets, expert_order, sorted_token, sorted_flat, flat_to_sorted,
+                         status, (int32_t*)workspace, (hipStream_t)stream);
+}
+
+// ───────────────────────── allocation-free dispatch ─────────────────────────
+// For callers that cannot allocate device memory (code under HIP graph capture, serving loops):
+// the histogram lives in a file-scope device array instead of a caller workspace. Each GPU holds
+// its own copy for the life of the process; its device address is looked up once per device with
+// hipGetSymbolAddress (the array's name is only a host-side stand-in in host code).
+constexpr size_t DISPATCH_SCRATCH_BYTES = (size_t)4 << 20;  // 4 MiB: nchunks * E <= 2^20
+static __device__ __align__(256) int32_t scratch[DISPATCH_SCRATCH_BYTES / sizeof(int32_t)];
+
+static std::mutex g_scratch_mu;
+static std::unordered_map<int, int32_t*> g_scratch_ptr;  // device ordinal -> device address
+
+static int32_t* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it != g_scratch_ptr.end()) return it->second;
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+  g_scratch_ptr[dev] = (int32_t*)ptr;
+  return (int32_t*)ptr;
+}
+
+extern "C" int moe_dispatch_noalloc(const int64_t* top_k_indices, int64_t n_tokens, int top_k,
+                                    int n_experts, int32_t* counts, int32_t* offsets,
+                                    int32_t* tile_offsets, int32_t* expert_order,
+                                    int32_t* sorted_token, int32_t* sorted_flat,
+                                    int32_t* flat_to_sorted, int32_t* status, void* stream) {
+  int st = dispatch_check(top_k_indices, n_tokens, top_k, n_experts, counts, offsets, tile_offsets,
+                          expert_order, sorted_token, sorted_flat, flat_to_sorted, status);
+  if (st) return st;
+  if (moe_get_workspace_size(n_tokens, top_k, n_experts) > DISPATCH_SCRATCH_BYTES)
+    return MOE_ERR_WORKSPACE;
+  int32_t* hist = scratch_for_current_device();
+  if (!hist) return MOE_ERR_LAUNCH;
+  return dispatch_launch(top_k_indices, n_tokens * top_k, top_k, n_experts, counts, offsets,
+                         tile_offsets, expert_order, sorted_token, sorted_flat, flat_to_sorted,
+                         status, hist, (hipStream_t)stream);
 }

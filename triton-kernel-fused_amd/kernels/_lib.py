@@ -28,6 +28,7 @@ _SIGS = {
     "moe_get_workspace_size": [_L, _I, _I],
     "moe_token_split_workspace_size": [],
     "moe_dispatch": [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _P],
+    "moe_dispatch_noalloc": [_P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "moe_grouped_gateup_swiglu_fwd": [_I, _P, _L, _L, _P, _I, _L, _P, _P, _P, _P, _L, _P, _P, _P,
                                       _P, _P],
     "moe_grouped_down_fwd": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P, _S, _P],
