@@ -753,16 +753,20 @@ token_gemm_v4_kernel(TokenArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     int* s_flag = (int*)smem;  // the ring is idle between the K loop and the epilogue
+    // Handoff: every thread of every piece wrote its partials and ran an agent-scope release
+    // fence (L2 write-back) before the barrier; thread 0 then counts the piece in. In the last
+    // piece every thread runs its own agent-scope acquire (vector-cache invalidate) after the
+    // barrier that publishes the flag, so each thread's partial reads below are ordered after
+    // the other pieces' releases without relying on one thread's fence covering the whole CU.
     if (threadIdx.x == 0) {
-      const int old = __hip_atomic_fetch_add(a.split_cnt + slot0, 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-      if (old == S - 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      *s_flag = old;
+      *s_flag = __hip_atomic_fetch_add(a.split_cnt + slot0, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     const bool last = *s_flag == S - 1;
     __syncthreads();  // every wave has read the flag before the epilogue reuses the LDS
     if (!last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     V4Sh16::zero(acc);
     for (int q = 0; q < S; ++q) {
 #pragma unroll

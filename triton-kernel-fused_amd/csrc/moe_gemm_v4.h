@@ -246,6 +246,9 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   // refill to the next step (FB == 2); fp8 and 16x16x32 tiles roll the A fragments and
   // double-buffer B (ROLL), every refill in the synchronising slab.
   constexpr bool ROLL = FR == 16 || CPL > 1;
+  // Only the ROLL schedule has a non-computing copy; the FB == 2 schedule always reads fragments
+  // and issues its MFMAs.
+  static_assert(COMPUTE || ROLL, "COMPUTE = false is implemented for the ROLL schedule only");
   constexpr int NM = TI_ * TJ_;  // MFMAs per slab
   const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;

@@ -117,19 +117,30 @@ def ptr(t):
 
 
 _SPLIT_WS = {}
+_SPLIT_WS_MAX = 4   # workspaces kept (one per (device, stream)); older ones are dropped
 
 
 def split_workspace(device):
     """The token GEMMs' split workspace for `device` and its current stream: zero-filled once and
     kept zero by the kernels; one per stream, since calls that share one must be stream-ordered.
+    At most _SPLIT_WS_MAX are kept (least recently used dropped), so code that makes a new stream
+    per iteration does not accumulate them; a dropped workspace is freed through the caching
+    allocator, which orders its reuse after the work already queued on that stream.
     Returns (pointer, bytes)."""
-    key = (torch.device(device).index, stream_of(device))
-    ws = _SPLIT_WS.get(key)
+    dev = torch.device(device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    key = (dev.index, stream_of(dev))
+    ws = _SPLIT_WS.pop(key, None)
     if ws is None:
-        n = lib().moe_token_split_workspace_size()
+        with torch.cuda.device(dev):
+            n = lib().moe_token_split_workspace_size()
         if n == 0:
             return None, 0
-        ws = _SPLIT_WS[key] = torch.zeros(n, device=device, dtype=torch.uint8)
+        ws = torch.zeros(n, device=dev, dtype=torch.uint8)
+    _SPLIT_WS[key] = ws                      # most recently used last
+    while len(_SPLIT_WS) > _SPLIT_WS_MAX:
+        del _SPLIT_WS[next(iter(_SPLIT_WS))]
     return ws.data_ptr(), ws.numel()
 
 
