@@ -53,13 +53,13 @@ def _traffic(kernel, workload):
         return None
 
 
-def run_bf16(config, steps, warmup, timer=True):
+def run_bf16(config, steps, warmup, timer=True, router=None):
     import torch
     import kernels
     from kernels import _lib
     from kernels.workloads import make_workload, flops
 
-    wl = make_workload(config, device="cuda", seed=0)
+    wl = make_workload(config, device="cuda", seed=0, scale=dict(router=router) if router else None)
     cfg = wl["cfg"]
     leaves = [wl[k].detach().requires_grad_(True) for k in ("hidden", "wt", "gate_up_proj", "down_proj")]
     idx, codes, dy = wl["idx"], wl["act_codes"], wl["grad_out"]
@@ -207,21 +207,80 @@ def cpu_baseline(config, sample_tokens, reps=3):
     cfg = wl["cfg"]
     args = [wl[k].float() for k in ("hidden", "idx", "wt", "gate_up_proj", "down_proj")]
     args[1] = wl["idx"]
-    times = []
-    for r in range(reps + 1):
-        t0 = time.perf_counter()
-        orc.moe_fwd_bwd(*args, [0] * cfg["E"], wl["grad_out"].float())
-        dt = time.perf_counter() - t0
-        if r:
-            times.append(dt)
-        _log(f"cpu rep {r}: {dt:.2f}s")
-    med = statistics.median(times)
+    med = _cpu_median(lambda: orc.moe_fwd_bwd(*args, [0] * cfg["E"], wl["grad_out"].float()),
+                      reps, f"config {config}")
     f = flops(cfg)
     return {"value": round(f / med / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": (f"config {config} routing/weights with N={sample_tokens} tokens "
                        f"(M={sample_tokens * cfg['k']} rows), fp32 fwd+bwd, median of {reps} after 1 "
                        f"warmup; os.cpu_count()={os.cpu_count()}")}
+
+
+def _cpu_median(fn, reps, tag):
+    times = []
+    for r in range(reps + 1):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        if r:
+            times.append(dt)
+        _log(f"cpu {tag} rep {r}: {dt:.2f}s")
+    return statistics.median(times)
+
+
+def cpu_baseline_lowp(config, sample_tokens, reps=3, scale=None):
+    """fp8 (config 4) / MXFP8 (config 5) forwards of the oracle on the host cores: each expert's
+    quantised weights are dequantised to fp32 inside the expert loop (config 5's dequantised
+    weights would not fit in host memory at once), fp32 math. Config 4 in TFLOP/s (6*M*H*I), config
+    5 in GB/s of the sample's algorithmic bytes (touched experts' e4m3 + E8M0 bytes, x, out,
+    routing), the units of the GPU lines."""
+    import torch
+    from kernels.workloads import make_workload, flops
+    from oracle import moe_oracle as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    # drawn and quantised on the GPU (config 5's fp32 weights are 45 GB), then copied to the host
+    gen = "cuda" if torch.cuda.is_available() else "cpu"
+    w = make_workload(config, device=gen, seed=0, scale=scale)
+    w = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in w.items()}
+    if gen == "cuda":
+        torch.cuda.empty_cache()
+    cfg = dict(w["cfg"], N=sample_tokens)
+    n, h, i, k = sample_tokens, cfg["H"], cfg["I"], cfg["k"]
+    idx, wt = w["idx"][:n], w["wt"][:n]
+    if config == 4:
+        fn = lambda: orc.fp8_forward(w["x_q"][:n], w["x_scale"][:n], idx, wt, w["gate_up_q"],
+                                     w["gate_up_scale"], w["down_q"], w["down_scale"])
+    else:
+        fn = lambda: orc.mxfp8_forward(w["hidden"][:n], idx, wt, w["gate_up_q"],
+                                       w["gate_up_scale"], w["down_q"], w["down_scale"])
+    med = _cpu_median(fn, reps, f"config {config}")
+    out = {"cores": torch.get_num_threads(), "kind": "port",
+           "sample": (f"config {config} full weights, first {n} of {w['cfg']['N']} tokens "
+                      f"(M={n * k} rows), fp32 fwd with per-expert dequantisation, median of {reps} "
+                      f"after 1 warmup; os.cpu_count()={os.cpu_count()}")}
+    if config == 4:
+        out.update(value=round(flops(cfg, backward=False) / med / 1e12, 4), unit="TFLOP/s")
+    else:
+        touched = int(torch.unique(idx).numel())
+        b = touched * 3 * h * i * (1 + 1 / 32) + 2 * n * h * 2 + n * k * (8 + 2)
+        out.update(value=round(b / med / 1e9, 2), unit="GB/s", touched_experts=touched)
+    return out
+
+
+def routing_stats(config, router=None):
+    """Group sizes of a config's routing: max, median of the non-empty, empty count, and the share
+    of routed rows on the 8 largest experts."""
+    import torch
+    from kernels.workloads import make_workload
+    w = make_workload(config, device="cpu", gen_device="cpu",
+                      scale=dict(H=8, I=8, **({"router": router} if router else {})))
+    e = w["cfg"]["E"]
+    c = torch.bincount(w["idx"].reshape(-1), minlength=e)
+    return {"max_rows": int(c.max()), "median_nonempty_rows": int(c[c > 0].median()),
+            "empty_experts": int((c == 0).sum()),
+            "top8_share": round(float(c.sort(descending=True).values[:8].sum() / c.sum()), 3)}
 
 
 def main():
@@ -296,11 +355,27 @@ def main():
         line["extra_configs"]["fp8_fwd"] = run_fp8(max(5, args.steps // 2), 2)
         _log("extra config 5 (MXFP8 decode)")
         line["extra_configs"]["mxfp8_decode"] = run_mxfp8(max(10, args.steps), 3)
+        for router, label in (("zipf_power_sigmoid", "many_experts_zipf_power"),
+                              ("uniform_topk_sigmoid", "many_experts_uniform")):
+            _log(f"extra config 3 routing {router}")
+            r3 = run_bf16(3, max(5, args.steps // 2), 2, timer=False, router=router)
+            line["extra_configs"][label] = {
+                "tflops": round(r3["tflops"], 2), "ms_per_step": round(r3["ms"], 4),
+                "frac_of_peak": round(r3["tflops"] / PEAK_BF16_TFLOPS, 4),
+                "routing": dict(router=router, **routing_stats(3, router))}
+        line["extra_configs"]["many_experts_zipf_routing"] = routing_stats(3)
         _log("extra: router epilogue")
         line["extra_configs"]["router_epilogue"] = run_router(max(10, args.steps), 3)
     if not args.no_cpu:
         _log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_tokens)
+        if not args.no_extra:
+            other = 2 if args.config != 2 else 3
+            line["cpu_baseline"]["other_configs"] = {
+                f"config{other}": cpu_baseline(other, 512 if other == 2 else args.cpu_tokens),
+                "config4": cpu_baseline_lowp(4, 1024),
+                "config5": cpu_baseline_lowp(5, 16),
+            }
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

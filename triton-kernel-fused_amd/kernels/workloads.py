@@ -14,6 +14,10 @@ down_proj, router, dY.
 Config 3's bias: experts are ranked by a seeded random permutation (rank 1..E) and expert e gets
 bias c * ln(rank_e^-1.2) with c = ZIPF_C = 1.75 (a Zipf(1.2) popularity on a log scale). The top
 ranks are picked by nearly every token and the tail by almost none, so group sizes span 0..N.
+
+Routing variants of config 3's shapes (same N, H, I, E, k, sigmoid gates), for robustness lines:
+  router="zipf_power_sigmoid"  bias c * rank^-1.2 (the power form, c = ZIPF_C): milder skew
+  router="uniform_topk_sigmoid" Gaussian logits only: near-uniform groups
 """
 import math
 
@@ -66,6 +70,14 @@ def _route(cfg, hidden, g, dev):
         rank = torch.randperm(e, generator=g, device=dev).float() + 1.0
         bias = ZIPF_C * torch.log(rank ** -ZIPF_ALPHA)
         w, idx = torch.topk(torch.sigmoid(logits + bias), k, dim=-1)
+    elif kind == "zipf_power_sigmoid":
+        logits = torch.randn(n, e, generator=g, device=dev)
+        rank = torch.randperm(e, generator=g, device=dev).float() + 1.0
+        bias = ZIPF_C * rank ** -ZIPF_ALPHA
+        w, idx = torch.topk(torch.sigmoid(logits + bias), k, dim=-1)
+    elif kind == "uniform_topk_sigmoid":
+        logits = torch.randn(n, e, generator=g, device=dev)
+        w, idx = torch.topk(torch.sigmoid(logits), k, dim=-1)
     elif kind == "uniform_sigmoid":
         logits = torch.randn(n, e, generator=g, device=dev)
         choice = torch.rand(n, e, generator=g, device=dev)
