@@ -117,8 +117,12 @@ __device__ __forceinline__ i32x4 ldg16(const void* p) { return *(const i32x4*)p;
 __device__ __forceinline__ void stg16(void* p, i32x4 v) { *(i32x4*)p = v; }
 __device__ __forceinline__ i32x4 zero4() { return i32x4{0, 0, 0, 0}; }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
-__device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }
+// sigma(g) = 1 / (1 + e^-g) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE
+// division sequence; e^-g = inf gives 0, so silu(-inf..) -> -0 as with a division.
+__device__ __forceinline__ float sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+__device__ __forceinline__ float silu(float g) { return g * sigmoid(g); }
 
 // Compile-time loop: f(std::integral_constant<int, i>) for i in [I, N). Each iteration is its own
 // code instance, so arrays indexed by the loop variable stay in registers however large the body.

@@ -248,8 +248,10 @@ __device__ __forceinline__ void token_epilogue(f32x16 (&acc)[C::TI][C::TJ], cons
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             go[j] = round_through<T>(acc[ti][tj][4 * g + j]);
-            dg[j] = go[j] * uv[g][j] * glu_dact(code, gv[g][j]);
-            du[j] = go[j] * glu_act(code, gv[g][j]);
+            float act, dact;
+            glu_act_dact(code, gv[g][j], act, dact);
+            dg[j] = go[j] * uv[g][j] * dact;
+            du[j] = go[j] * act;
           }
           if (i0 < a.I) {
             if (gi) Store4<T>::st(gi + i0, go[0], go[1], go[2], go[3]);
@@ -494,7 +496,11 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
     float* part = a.part + (size_t)(2 * rt + wr) * a.out_ld;  // out_ld = M (partials row length)
     // Rows per batch of gate_up loads: 4 measured ~1% faster than 8 and ~4% faster than all 16 at
     // once (the epilogues of all CUs compete for HBM).
+#ifdef MOE_GATED_NB
+    constexpr int NB = MOE_GATED_NB;
+#else
     constexpr int NB = 4;
+#endif
 #pragma unroll 1
     for (int i0 = 0; i0 < WQ / 4; i0 += NB) {
       i32x4 gq[NB], uq[NB];
@@ -503,8 +509,13 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
       for (int b = 0; b < NB; ++b) {
         const int m = min(row0 + (i0 + b) * 4 + (lane >> 4), m_end - 1);
         const T* r = gu + (size_t)m * 2 * a.I + chc;
+#ifdef MOE_EXP_NOLOAD
+        gq[b] = i32x4{m, chc, 0, 0};
+        uq[b] = i32x4{0, m, chc, 0};
+#else
         gq[b] = *(const i32x4*)r;
         uq[b] = *(const i32x4*)(r + a.I);
+#endif
         wv[b] = __shfl(wrow, (i0 + b) * 4 + (lane >> 4), 64);
       }
 #pragma unroll
@@ -519,18 +530,23 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
         float dot = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float act = glu_act(code, gv[j]);
+          float act, dact;
+          glu_act_dact(code, gv[j], act, dact);
           const float inter = act * uv[j];
           dot += cok ? go[j] * inter : 0.f;
           const float gi = wv[b] * go[j];
-          dg[j] = gi * uv[j] * glu_dact(code, gv[j]);
+          dg[j] = gi * uv[j] * dact;
           du[j] = gi * act;
           ia[j] = wv[b] * inter;
         }
         // The row's 16 lanes (channels 8c .. 8c+7 each) sum their partial dots.
 #pragma unroll
         for (int d = 1; d < 16; d <<= 1) dot += __shfl_xor(dot, d, 64);
+#ifdef MOE_EXP_NOSTORE
+        if (m < m_end && dot == 12345.f) {
+#else
         if (m < m_end) {
+#endif
           if (c == 0) part[m] = dot;
           if (cok) {
             if (ggu) {
@@ -578,8 +594,10 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
             v2::unpack8<T>(uq[b], uv);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-              dg[j] = go[j] * uv[j] * glu_dact(code, gv[j]);
-              du[j] = go[j] * glu_act(code, gv[j]);
+              float act, dact;
+              glu_act_dact(code, gv[j], act, dact);
+              dg[j] = go[j] * uv[j] * dact;
+              du[j] = go[j] * act;
             }
             T* r = ggu + (size_t)m * 2 * a.I + ch;
             v2::st_stream(v2::pack8<T>(dg), r);
@@ -625,6 +643,18 @@ struct V4Shape {
 using V4Sh16 = V4Shape<f32x4, v4::TI16, v4::TJ16, 16, v4::KcLoad16>;
 using V4Sh32 = V4Shape<f32x16, v4::TI, v4::TJ, 32, v4::KcLoad>;
 
+// Phase timestamps for experiments (built only with -DMOE_PHASE_TRACE): per workgroup, the
+// 100 MHz wall clock at kernel start, K-loop start, K-loop end and epilogue end.
+#ifdef MOE_PHASE_TRACE
+__device__ unsigned long long g_phase[16 * 65536 * 4];
+#define MOE_PHASE(slot, i)                                                                   \
+  do {                                                                                       \
+    if (threadIdx.x == 0) g_phase[((size_t)(slot) * 65536 + blockIdx.x) * 4 + (i)] = wall_clock64(); \
+  } while (0)
+#else
+#define MOE_PHASE(slot, i) do {} while (0)
+#endif
+
 // Token GEMMs on the eight-wave ring kernel of moe_gemm_v4.h. The token side Q is K-contiguous
 // (gathered or sorted rows); the weights P are K-contiguous in the forward and row-contiguous
 // (P_RC) in the dX GEMMs.
@@ -633,6 +663,14 @@ __global__ void __launch_bounds__(v4::NT, 1)
 token_gemm_v4_kernel(TokenArgs a) {
   using C = V2Cfg<T>;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
+  constexpr int PH = EPI * 2 + (P_RC ? 1 : 0);
+  MOE_PHASE(PH, 0);
+#ifdef MOE_STAGGER_US
+  if (blockIdx.x < 256 && ((blockIdx.x >> 3) & 1)) {
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < (unsigned long long)(MOE_STAGGER_US * 100)) __builtin_amdgcn_s_sleep(32);
+  }
+#endif
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
@@ -718,6 +756,7 @@ token_gemm_v4_kernel(TokenArgs a) {
     lp.kend = a.K;
     lp.init(wr * v4::WP, a.R - r0);
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
+    MOE_PHASE(PH, 1);
     if (wave_rows) v4::mainloop_ring<T, true>(acc, lp, lq, kb, ke, smem);
     else v4::mainloop_ring<T, false>(acc, lp, lq, kb, ke, smem);
   } else {
@@ -737,9 +776,11 @@ token_gemm_v4_kernel(TokenArgs a) {
       lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
     }
     v4::bare_barrier();  // s_pref is read; the LDS now belongs to the K loop (LDS-only)
+    MOE_PHASE(PH, 1);
     if (wave_rows) v4::mainloop_ring<T, true>(acc, lp, lq, kb, ke, smem);
     else v4::mainloop_ring<T, false>(acc, lp, lq, kb, ke, smem);
   }
+  MOE_PHASE(PH, 2);
   if (S > 1) {
     // Split piece: every piece stores its partial tile and, after a device-scope release, counts
     // itself in; the last to arrive acquires, sums all pieces in piece order (the same result
@@ -780,6 +821,11 @@ token_gemm_v4_kernel(TokenArgs a) {
     if (a.gate) wrow = to_f32(__builtin_bit_cast(T, wbits));
   }
   token_epilogue_v2<T, EPI, v4::WQ>(acc, a, e, m0, m_end, rt, smem, wr, wc, wrow);
+#ifdef MOE_PHASE_TRACE
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+#endif
+  MOE_PHASE(PH, 3);
 }
 
 // Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
@@ -1250,3 +1296,14 @@ extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, cons
     default: return go.template operator()<float>();
   }
 }
+
+#ifdef MOE_PHASE_TRACE
+extern "C" int moe_phase_read(void* host, size_t bytes) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+extern "C" int moe_phase_reset(void) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_phase)) != hipSuccess) return 1;
+  return hipMemset(p, 0, sizeof(g_phase)) == hipSuccess ? 0 : 1;
+}
+#endif

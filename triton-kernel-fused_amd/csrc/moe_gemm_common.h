@@ -81,6 +81,18 @@ __device__ __forceinline__ float glu_dact(int code, float g) {
   const float s = sigmoid(g);
   return s * (1.f + g * (1.f - s));
 }
+// act(g) and act'(g) together (one sigmoid for SiLU).
+__device__ __forceinline__ void glu_act_dact(int code, float g, float& act, float& dact) {
+  if (code == 1) {
+    const float r = fmaxf(g, 0.f);
+    act = r * r;
+    dact = 2.f * r;
+  } else {
+    const float s = sigmoid(g);
+    act = g * s;
+    dact = s * (1.f + g * (1.f - s));
+  }
+}
 
 // ---------------------------------------------------------------------------------------------
 // Token-grouped GEMM: for each expert e < E_glu and each tile of its sorted rows,
