@@ -496,11 +496,7 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
     float* part = a.part + (size_t)(2 * rt + wr) * a.out_ld;  // out_ld = M (partials row length)
     // Rows per batch of gate_up loads: 4 measured ~1% faster than 8 and ~4% faster than all 16 at
     // once (the epilogues of all CUs compete for HBM).
-#ifdef MOE_GATED_NB
-    constexpr int NB = MOE_GATED_NB;
-#else
     constexpr int NB = 4;
-#endif
 #pragma unroll 1
     for (int i0 = 0; i0 < WQ / 4; i0 += NB) {
       i32x4 gq[NB], uq[NB];
@@ -509,13 +505,8 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
       for (int b = 0; b < NB; ++b) {
         const int m = min(row0 + (i0 + b) * 4 + (lane >> 4), m_end - 1);
         const T* r = gu + (size_t)m * 2 * a.I + chc;
-#ifdef MOE_EXP_NOLOAD
-        gq[b] = i32x4{m, chc, 0, 0};
-        uq[b] = i32x4{0, m, chc, 0};
-#else
         gq[b] = *(const i32x4*)r;
         uq[b] = *(const i32x4*)(r + a.I);
-#endif
         wv[b] = __shfl(wrow, (i0 + b) * 4 + (lane >> 4), 64);
       }
 #pragma unroll
@@ -542,11 +533,7 @@ __device__ __forceinline__ void token_epilogue_v2(const Acc& acc, const TokenArg
         // The row's 16 lanes (channels 8c .. 8c+7 each) sum their partial dots.
 #pragma unroll
         for (int d = 1; d < 16; d <<= 1) dot += __shfl_xor(dot, d, 64);
-#ifdef MOE_EXP_NOSTORE
-        if (m < m_end && dot == 12345.f) {
-#else
         if (m < m_end) {
-#endif
           if (c == 0) part[m] = dot;
           if (cok) {
             if (ggu) {
@@ -665,12 +652,6 @@ token_gemm_v4_kernel(TokenArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
   constexpr int PH = EPI * 2 + (P_RC ? 1 : 0);
   MOE_PHASE(PH, 0);
-#ifdef MOE_STAGGER_US
-  if (blockIdx.x < 256 && ((blockIdx.x >> 3) & 1)) {
-    const unsigned long long t0 = wall_clock64();
-    while (wall_clock64() - t0 < (unsigned long long)(MOE_STAGGER_US * 100)) __builtin_amdgcn_s_sleep(32);
-  }
-#endif
   // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
   int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
   tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
@@ -828,6 +809,331 @@ token_gemm_v4_kernel(TokenArgs a) {
   MOE_PHASE(PH, 3);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Persistent token GEMMs (no K split). One workgroup per CU slot of an XCD runs the XCD's logical
+// tiles bi, bi + n_wg, bi + 2 n_wg, ... (the same tiles the XCD's CUs ran at once in the
+// one-tile-per-workgroup kernel above, so the L2 sharing is unchanged). That kernel spends ~2.5 us
+// per tile on set-up (the expert tile scan and its barrier, token-row indices) before the ring's
+// first loads; here the next tile's expert comes from a scalar walk over the offsets (no barrier,
+// no vector memory access) and only its token-row indices are loaded. The epilogue stages 16
+// token rows at a time through ring slot 0 (4 KB per wave); each tile's ring starts at slot 1.
+// Measured on config 3: gate/up forward -4.7%, down forward -4.3%, gated down dX -1.4%, gate/up
+// dX -1%.
+namespace v5 {
+constexpr int BASE = 1;            // ring slot of each tile's P0
+constexpr int STAGE_B = 4096;      // per-wave staging: 16 rows x 256 bytes
+static_assert(v4::NW * STAGE_B == v4::SLOTB, "the staging of all waves is ring slot 0");
+
+// Expert lookup of token tiles from the sorted-row offsets, in scalar registers: a walk over the
+// experts that resumes where the previous lookup stopped (a workgroup's token tiles come in
+// non-decreasing order when its tile stride is a multiple of the tile group; otherwise the walk
+// restarts). The offsets are read with scalar loads (scalar cache, counted apart from the vector
+// memory operations whose waits the ring relies on).
+struct Experts {
+  const int32_t* off;
+  int E;
+  int n_mt;     // token tiles in total
+  int e, pref;  // walk state: expert e and the index of its first token tile
+  __device__ __forceinline__ void init(const int32_t* offsets, int n_experts) {
+    off = offsets;
+    E = n_experts;
+    const int l = v4::lane_id();
+    int tot = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int x = base + l;
+      int c = x < E ? (offsets[x + 1] - offsets[x] + v4::TILE - 1) / v4::TILE : 0;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) c += __shfl_xor(c, d, 64);
+      tot += c;
+    }
+    n_mt = __builtin_amdgcn_readfirstlane(tot);
+    e = 0;
+    pref = 0;
+  }
+  // Expert of token tile mt (< n_mt) and its rows [m0, m_end).
+  __device__ __forceinline__ void lookup(int mt, int& ex, int& m0, int& m_end) {
+    if (mt < pref) {
+      e = 0;
+      pref = 0;
+    }
+    int o0 = v3::sload(off + e), o1 = v3::sload(off + e + 1);
+    while (mt >= pref + (o1 - o0 + v4::TILE - 1) / v4::TILE) {
+      pref += (o1 - o0 + v4::TILE - 1) / v4::TILE;
+      ++e;
+      o0 = o1;
+      o1 = v3::sload(off + e + 1);
+    }
+    ex = e;
+    m0 = o0 + (mt - pref) * v4::TILE;
+    m_end = o1;
+  }
+};
+
+struct Tile {
+  int e, m0, m_end, rt;
+};
+
+// Accumulator rows tj*16 .. tj*16+15 of the wave (16x16 MFMA tiles: lane l holds channels
+// ti*16 + 4(l/16) + v of row l%16) to the wave's staging block, rounded to T.
+template <typename T, int TI_, int TJ_>
+__device__ __forceinline__ void stage_rows(const f32x4 (&acc)[TI_][TJ_], int tj, char* wl) {
+  const int lane = v4::lane_id(), h = (lane >> 4) & 1, g = lane >> 5;
+  const int q = lane & 15;
+#pragma unroll
+  for (int ti = 0; ti < TI_; ++ti) {
+    uint2 v = {v2::pack2<T>(acc[ti][tj][0], acc[ti][tj][1]),
+               v2::pack2<T>(acc[ti][tj][2], acc[ti][tj][3])};
+    *(uint2*)(wl + v2::staged_off(q, 2 * ti + g) + 8 * h) = v;
+  }
+}
+
+// Epilogue of one tile: the token_epilogue_v2 operations, 16 rows per pass through the wave's
+// staging block.
+template <typename T, int EPI, class Acc>
+__device__ __forceinline__ void epilogue(const Acc& acc, const TokenArgs& a, const Tile& t,
+                                         char* wl, int wr, int wc, float wrow) {
+  const int lane = v4::lane_id();
+  const int row0 = t.m0 + wc * v4::WQ;
+  const bool rows = row0 < t.m_end;  // false: this wave's token rows all lie past the group end
+  const int code = (EPI != EPI_STORE && a.act_codes) ? a.act_codes[t.e] : 0;
+  static_for<0, V4Sh16::TJ>([&](auto tjc) {
+    constexpr int TJ = decltype(tjc)::value;
+    const bool live = rows && row0 + TJ * 16 < t.m_end;
+    if constexpr (EPI == EPI_STORE) {
+      if (!live) return;
+      stage_rows<T>(acc, TJ, wl);
+      const int c = lane & 15;
+      const int ch = t.rt * v4::TILE + wr * v2::WT + 8 * c;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int q = it * 4 + (lane >> 4);
+        const int m = row0 + TJ * 16 + q;
+        const i32x4 v = v2::staged(wl, q, c);
+        if (m < t.m_end && ch < a.R) v2::st_stream(v, (T*)a.out + (size_t)m * a.out_ld + ch);
+      }
+    } else if constexpr (EPI == EPI_GLU_FWD) {
+      if (!live) return;
+      stage_rows<T>(acc, TJ, wl);
+      const int c = lane & 7;
+      const int ch = t.rt * (v2::TILE / 2) + wr * (v2::WT / 2) + 8 * c;
+      T* gu = (T*)a.out;
+      T* it = (T*)a.out2;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int q = i * 8 + (lane >> 3);
+        const int m = row0 + TJ * 16 + q;
+        const i32x4 gq = v2::staged(wl, q, c), uq = v2::staged(wl, q, c + 8);
+        const float w = __shfl(wrow, TJ * 16 + q, 64);  // every lane active
+        if (m < t.m_end && ch < a.I) {
+          T* r = gu + (size_t)m * 2 * a.I + ch;
+          v2::st_stream(gq, r);
+          v2::st_stream(uq, r + a.I);
+          if (it) {
+            float gv[8], uv[8], iv[8];
+            v2::unpack8<T>(gq, gv);
+            v2::unpack8<T>(uq, uv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) iv[j] = w * (glu_act(code, gv[j]) * uv[j]);
+            v2::st_stream(v2::pack8<T>(iv), it + (size_t)m * a.I + ch);
+          }
+        }
+      }
+    } else if constexpr (EPI == EPI_GLU_BWD_GATED) {
+      if (!live) return;
+      stage_rows<T>(acc, TJ, wl);
+      const int c = lane & 15;
+      const int ch = t.rt * v2::TILE + wr * v2::WT + 8 * c;
+      const int chc = min(ch, a.I - 8);
+      const bool cok = ch < a.I;
+      const T* gu = (const T*)a.aux;
+      T* ggu = (T*)a.out;
+      T* iw = (T*)a.out2;
+      float* part = a.part + (size_t)(2 * t.rt + wr) * a.out_ld;
+      i32x4 gq[4], uq[4];
+      float wv[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int q = b * 4 + (lane >> 4);
+        const int m = min(row0 + TJ * 16 + q, t.m_end - 1);
+        const T* r = gu + (size_t)m * 2 * a.I + chc;
+        gq[b] = *(const i32x4*)r;
+        uq[b] = *(const i32x4*)(r + a.I);
+        wv[b] = __shfl(wrow, TJ * 16 + q, 64);
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int q = b * 4 + (lane >> 4);
+        const int m = row0 + TJ * 16 + q;
+        const i32x4 oq = v2::staged(wl, q, c);
+        float go[8], gv[8], uv[8], dg[8], du[8], ia[8];
+        v2::unpack8<T>(oq, go);
+        v2::unpack8<T>(gq[b], gv);
+        v2::unpack8<T>(uq[b], uv);
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float act, dact;
+          glu_act_dact(code, gv[j], act, dact);
+          const float inter = act * uv[j];
+          dot += cok ? go[j] * inter : 0.f;
+          const float gi = wv[b] * go[j];
+          dg[j] = gi * uv[j] * dact;
+          du[j] = gi * act;
+          ia[j] = wv[b] * inter;
+        }
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) dot += __shfl_xor(dot, d, 64);
+        if (m < t.m_end) {
+          if (c == 0) part[m] = dot;
+          if (cok) {
+            if (ggu) {
+              T* r = ggu + (size_t)m * 2 * a.I + ch;
+              v2::st_stream(v2::pack8<T>(dg), r);
+              v2::st_stream(v2::pack8<T>(du), r + a.I);
+            }
+            if (iw) v2::st_stream(v2::pack8<T>(ia), iw + (size_t)m * a.I + ch);
+          }
+        }
+      }
+    }
+  });
+}
+}  // namespace v5
+
+template <typename T, int EPI, bool P_RC>
+__global__ void __launch_bounds__(v4::NT, 1)
+token_gemm_v5_kernel(TokenArgs a) {
+  using C = V2Cfg<T>;
+  using LQ = typename V4Sh16::Kc;
+  using LP = std::conditional_t<P_RC, v4::RcLoad<false, V4Sh16::TI, V4Sh16::FR>, typename V4Sh16::Kc>;
+  constexpr bool WGATE = EPI == EPI_GLU_BWD_GATED || EPI == EPI_GLU_FWD;
+  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  v5::Experts ex;
+  ex.init(a.offsets, a.E_glu);
+  const int gm = v4::tile_group(a.n_rtiles);
+  const int n_idx = (ex.n_mt + gm - 1) / gm * gm * a.n_rtiles;
+  const int x = (int)blockIdx.x & 7, bi = (int)blockIdx.x >> 3, nwg = (int)gridDim.x >> 3;
+  const int R = (n_idx + 7) >> 3;
+  const int t_lo = x * R, t_cnt = max(0, min(n_idx, t_lo + R) - t_lo);
+  const int wr = v4::wave_r(), wc = v4::wave_c();
+
+  // First valid logical tile at local index j or later (stride nwg); t_cnt if none.
+  auto find = [&](int j, v5::Tile& t) {
+    for (; j < t_cnt; j += nwg) {
+      int mt, rt;
+      v4::tile_of(t_lo + j, a.n_rtiles, mt, rt);
+      if (mt < ex.n_mt) {
+        ex.lookup(mt, t.e, t.m0, t.m_end);
+        t.rt = rt;
+        return j;
+      }
+    }
+    return t_cnt;
+  };
+  // Operand row pointers (and the gate of this lane's token row) of tile t.
+  auto setup = [&](const v5::Tile& t, LP& lp, LQ& lq, unsigned short& wbits) {
+    const T* Pe = (const T*)a.P + (size_t)t.e * a.p_e;
+    if constexpr (WGATE) {
+      const int m = min(t.m0 + wc * v4::WQ + v4::lane_id(), t.m_end - 1);
+      const unsigned short* gp = (const unsigned short*)a.offsets;
+      if (a.gate) gp = (const unsigned short*)a.gate + (a.sflat ? a.sflat[m] : m);
+      wbits = *gp;
+    }
+    lq.init(wc * v4::WQ);
+#pragma unroll
+    for (int i = 0; i < v4::LOADS; ++i) {
+      int m = t.m0 + v4::KcLoad::row_of(i);
+      if (m >= t.m_end) m = t.m0;
+      const int qr = a.q_gather ? a.q_gather[m] : m;
+      lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
+    }
+    if constexpr (P_RC) {
+      const int r0 = t.rt * v4::TILE;
+      lp.src = (const char*)(Pe + r0);
+      lp.ld = (size_t)a.p_ld * sizeof(T);
+      lp.gather = nullptr;
+      lp.kend = a.K;
+      lp.init(wr * v4::WP, a.R - r0);
+    } else {
+      lp.init(wr * v4::WP);
+#pragma unroll
+      for (int i = 0; i < v4::LOADS; ++i) {
+        const int rr = v4::KcLoad::row_of(i);
+        bool ok;
+        int prow;
+        if (EPI == EPI_GLU_FWD) {
+          prow = glu_prow<C>(rr, t.rt, a.I, ok);
+        } else {
+          prow = t.rt * v4::TILE + rr;
+          ok = prow < a.R;
+        }
+        lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+      }
+    }
+  };
+
+  v5::Tile cur;
+  int j = find(bi, cur);
+  if (j >= t_cnt) return;
+  LP lp;
+  LQ lq;
+  unsigned short wbits = 0;
+  setup(cur, lp, lq, wbits);
+  v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
+  char* wl = smem + (threadIdx.x >> 6) * v5::STAGE_B;  // staging: ring slot 0
+#ifdef MOE_PHASE_TRACE
+  constexpr int PH = 8 + EPI * 2 + (P_RC ? 1 : 0);
+  int n_tile = 0;
+#define MOE_PHASE5(i)                                                                         \
+  do {                                                                                        \
+    if (threadIdx.x == 0 && n_tile < 64)                                                      \
+      g_phase[((size_t)PH * 65536 + blockIdx.x * 64 + n_tile) * 4 + (i)] = wall_clock64();     \
+  } while (0)
+#else
+#define MOE_PHASE5(i) do {} while (0)
+#endif
+  while (true) {
+    MOE_PHASE5(0);
+    v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, v4::NSLOT - 1, 1);  // P2 -> slot 0
+    typename V4Sh16::Acc acc[V4Sh16::TI][V4Sh16::TJ];
+    V4Sh16::zero(acc);
+    if (cur.m0 + wc * v4::WQ < cur.m_end)
+      v4::mainloop_ring<T, true, true>(acc, lp, lq, 0, a.K, smem, v5::BASE);
+    else
+      v4::mainloop_ring<T, false, true>(acc, lp, lq, 0, a.K, smem, v5::BASE);
+    // The ring is drained and every wave is past its last read: slots 1-4 take the next tile's
+    // first loads while this tile's epilogue stages through slot 0.
+    MOE_PHASE5(1);
+    v5::Tile nxt;
+    const int jn = find(j + nwg, nxt);
+    float wrow = 1.f;
+    if constexpr (WGATE) {
+      if (a.gate) wrow = to_f32(__builtin_bit_cast(T, wbits));
+    }
+    MOE_PHASE5(2);
+    v5::epilogue<T, EPI>(acc, a, cur, wl, wr, wc, wrow);
+#ifdef MOE_PHASE_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+    MOE_PHASE5(3);
+#ifdef MOE_PHASE_TRACE
+    ++n_tile;
+#endif
+    // The next tile's set-up and first ring loads (slots 1-4; nobody reads the ring between K
+    // loops), then the barrier that frees the staging slot for P2. Measured on config 3, issuing
+    // these loads during the epilogue instead gained nothing on the plain-store and forward
+    // epilogues and cost the gated one (its gate_up loads then wait behind them). The set-up runs
+    // for the last tile too (on valid, unused values): unconditional, it keeps the register
+    // allocation free of spills.
+    setup(jn < t_cnt ? nxt : cur, lp, lq, wbits);
+    if (jn < t_cnt) v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
+    if (jn >= t_cnt) break;
+    v4::bare_barrier();  // every wave is done with slot 0 before P2 lands in it
+    cur = nxt;
+    j = jn;
+  }
+}
+
 // Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
 // of rsrc[rrow(m), r] * csrc[crow(m), c]; both operands row-contiguous (optionally gathered rows).
 template <typename T, bool RG, bool CG>
@@ -980,8 +1286,20 @@ static int launch_wgrad(const WgradArgs& a, int E, hipStream_t s) {
 }
 
 
-// 256x256 token GEMMs: the eight-wave ring kernel when K is a multiple of its 64-value step,
-// otherwise (dX GEMMs with K a multiple of 32) the four-wave five-stage kernel.
+// CUs of the current device (cached per device ordinal; 0 on error).
+static int device_cus() {
+  static int cache[64];
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cache[dev] = n;
+  return n;
+}
+
+// 256x256 token GEMMs: the persistent ring kernel (up to 64 GLU experts, no K split), else the
+// one-tile-per-workgroup ring kernel when K is a multiple of its 64-value step, otherwise (dX
+// GEMMs with K a multiple of 32) the four-wave five-stage kernel.
 template <typename T, int EPI, bool P_RC>
 static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   a.n_rtiles = EPI == EPI_GLU_FWD ? (int)((a.I + v2::TILE / 2 - 1) / (v2::TILE / 2))
@@ -989,6 +1307,20 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
   const int64_t logical = v4::logical_tiles(max_mt, a.n_rtiles);
   if (logical <= 0 || n_rows == 0) return MOE_OK;
+#ifndef MOE_NO_PERSISTENT
+  const bool split = EPI == EPI_STORE && a.split_ws && a.K / 64 >= v4::SPLIT_MIN_STEPS;
+  const int cus = device_cus();
+  if constexpr (EPI != EPI_GLU_BWD) {
+  if (a.K % 64 == 0 && !split && cus >= 8) {
+    const int64_t per_xcd = (logical + 7) / 8;
+    const int64_t grid = 8 * std::min<int64_t>(cus / 8, per_xcd);
+    auto kern = token_gemm_v5_kernel<T, EPI, P_RC>;
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a);
+    return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
+  }
+  }
+#endif
   int64_t grid = (logical + 7) / 8 * 8;
   if (a.split_ws && a.K % 64 == 0) grid += 8 * (int64_t)a.xcd_cus;  // the split pieces
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
@@ -1103,12 +1435,6 @@ extern "C" int moe_grouped_gateup_swiglu_fwd(int dtype, const void* hidden, int6
 }
 
 // Workgroup slots of the current device (CUs; one 160 KB-LDS workgroup each).
-static int device_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return n;
-}
 
 extern "C" size_t moe_token_split_workspace_size(void) {
   const int n = device_cus();

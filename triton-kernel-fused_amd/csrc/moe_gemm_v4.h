@@ -127,7 +127,7 @@ struct RcLoad {
   int cbyte[2];       // column byte offsets for even / odd i (clamped inside the operand)
   int zoff[2];        // zero-block offsets of the same chunks
   int toff[NFRAG];    // fragment reads: byte offset of fragment t for slab 0
-  int gi[2 * LOADS];  // GATHER: row indices of this wave's K rows of the next issue
+  int gi[GATHER ? 2 * LOADS : 1];  // GATHER: row indices of this wave's K rows of the next issue
 
   // rbase: first column (r) of this wave's fragment block; rvalid: columns inside the operand.
   __device__ __forceinline__ void init(int rbase, int rvalid) {
@@ -233,9 +233,35 @@ __device__ __forceinline__ void wait_slots(int n) {
 // COMPUTE false (a wave whose token rows are all past the group end): the same loads and
 // barriers, no fragment reads and no MFMAs, so the SIMD's other wave has the LDS and the matrix
 // pipe to itself.
-template <typename T, bool COMPUTE = true, typename AccV, int TI_, int TJ_, class LP, class LQ>
+// Prologue DMAs of the ring over K in [k0, k1): loads [first, first + count) of the sequence
+// P0 Q0 P1 Q1 P2, load i into slot (base + i) % NSLOT. A persistent kernel issues the next tile's
+// first loads while the current tile's epilogue runs (mainloop_ring with PRE = true then skips
+// them).
+template <typename T, class LP, class LQ>
+__device__ __forceinline__ void ring_prologue(LP& lp, LQ& lq, int k0, int k1, char* smem, int base,
+                                              int first, int count) {
+  constexpr int KS = v2::bk<T>();
+  const int nk = (k1 - k0 + KS - 1) / KS;
+  const int klast = k0 + (nk - 1) * KS;
+  if (first == 0) {
+    lp.prime(k0);
+    lq.prime(k0);
+  }
+  for (int i = first; i < first + count; ++i) {
+    const int si = base + i >= NSLOT ? base + i - NSLOT : base + i;
+    char* slot = smem + si * SLOTB;
+    const int k = min(k0 + (i >> 1) * KS, klast);
+    if (i & 1) lq.template issue<T>(slot, k);
+    else lp.template issue<T>(slot, k);
+  }
+}
+
+// PRE: the caller has issued all NSLOT prologue loads with ring_prologue(..., base, ...) (and
+// possibly other memory operations after them, which the first wait then also covers).
+template <typename T, bool COMPUTE = true, bool PRE = false, typename AccV, int TI_, int TJ_,
+          class LP, class LQ>
 __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ& lq, int k0, int k1,
-                                              char* smem) {
+                                              char* smem, int base = 0) {
   constexpr int KS = v2::bk<T>();
   constexpr int CPL = Mfma<T>::CPL;
   constexpr int FR = sizeof(AccV) == sizeof(f32x4) ? 16 : 32;  // MFMA tile rows
@@ -253,20 +279,14 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   const int nk = (k1 - k0 + KS - 1) / KS;
   if (nk <= 0) return;
 
-  // Prologue: loads 0..NSLOT-1 (P0 Q0 P1 Q1 P2) into slots 0..4.
-  lp.prime(k0);
-  lq.prime(k0);
+  // Prologue: loads 0..NSLOT-1 (P0 Q0 P1 Q1 P2) into slots base .. base+4 (mod NSLOT).
   const int klast = k0 + (nk - 1) * KS;
   constexpr int PRO = ROLL ? NSLOT : NSLOT - 1;  // FB == 2: P2 goes out with step 0's slab 0
-  for (int i = 0; i < PRO; ++i) {
-    char* slot = smem + i * SLOTB;
-    const int k = min(k0 + (i >> 1) * KS, klast);
-    if (i & 1) lq.template issue<T>(slot, k);
-    else lp.template issue<T>(slot, k);
-  }
+  static_assert(!PRE || ROLL, "a pre-issued prologue is implemented for the ROLL schedule");
+  if constexpr (!PRE) ring_prologue<T>(lp, lq, k0, k1, smem, base, 0, PRO);
   wait_slots(PRO - 2);
   // Pending P refill (slot, K) issued during the next step's first slab.
-  int pp_slot = NSLOT - 1, pp_k = min(k0 + 2 * KS, klast);
+  int pp_slot = base == 0 ? NSLOT - 1 : base - 1, pp_k = min(k0 + 2 * KS, klast);
   bare_barrier();
 
   constexpr int FB = ROLL ? 1 : 2;
@@ -282,15 +302,15 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   };
   // ROLL: one A buffer, two B buffers.
   i32x4 ra[TI_][CPL], rb[2][TJ_][CPL];
-  int sp = 0, sq = 1;  // slots of P_s, Q_s
+  int sp = base, sq = base + 1 == NSLOT ? 0 : base + 1;  // slots of P_s, Q_s
   if constexpr (FB == 2) load(0, smem + sp * SLOTB, smem + sq * SLOTB, 0);
   if constexpr (ROLL) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-      for (int t = 0; t < TI_; ++t) ra[t][c] = lp.template frag<CPL>(smem, t, 0, c);
+      for (int t = 0; t < TI_; ++t) ra[t][c] = lp.template frag<CPL>(smem + sp * SLOTB, t, 0, c);
 #pragma unroll
-      for (int t = 0; t < TJ_; ++t) rb[0][t][c] = lq.template frag<CPL>(smem + SLOTB, t, 0, c);
+      for (int t = 0; t < TJ_; ++t) rb[0][t][c] = lq.template frag<CPL>(smem + sq * SLOTB, t, 0, c);
     }
     // lgkmcnt(0) (vmcnt and expcnt at their maxima) as a real waitcnt instruction, so the
     // compiler's loop-entry state holds no LDS reads and the in-loop waits stay partial.
