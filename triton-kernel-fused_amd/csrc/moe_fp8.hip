@@ -29,130 +29,157 @@ struct Fp8Args {
   long long out_ld;
 };
 
+// Persistent: one workgroup per CU slot of an XCD runs the XCD's logical tiles bi, bi + n_wg, ...
+// (as the bf16 persistent token GEMMs: a scalar expert walk instead of a per-tile scan, and the
+// next tile's ring loads issued as soon as the epilogue has released the LDS).
 template <bool GLU>
 __global__ void __launch_bounds__(v4::NT, 1)
 fp8_gemm_kernel(Fp8Args a) {
   using C = Cfg<fp8e4m3, v4::TILE, v4::TILE, 2, 2>;  // GLU row interleave per 128-row P half
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  // The expert tile scan borrows the last ring slot (free until the K loop's prologue).
-  int* s_pref = (int*)(smem + (v4::NSLOT - 1) * v4::SLOTB);
-  tile_prefix<v4::NT>(a.offsets, a.E_glu, v4::TILE, s_pref, s_pref + MAX_GLU_EXPERTS + 1);
-  int mt, rt;
-  if (!v4::block_tile(s_pref[a.E_glu], a.n_rtiles, mt, rt)) return;
-  int lo = 0, hi = a.E_glu - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (s_pref[mid] <= mt) lo = mid; else hi = mid - 1;
-  }
-  const int e = lo;
-  const int m0 = a.offsets[e] + (mt - s_pref[e]) * v4::TILE;
-  const int m_end = a.offsets[e + 1];
-  const fp8e4m3* Pe = a.P + (size_t)e * a.p_e;
+  v4::Experts ex;
+  ex.init(a.offsets, a.E_glu);
+  const int gm = v4::tile_group(a.n_rtiles);
+  const int n_idx = (ex.n_mt + gm - 1) / gm * gm * a.n_rtiles;
+  const int xcd = (int)blockIdx.x & 7, bi = (int)blockIdx.x >> 3, nwg = (int)gridDim.x >> 3;
+  const int R8 = (n_idx + 7) >> 3;
+  const int t_lo = xcd * R8, t_cnt = max(0, min(n_idx, t_lo + R8) - t_lo);
   const int wr = v4::wave_r(), wc = v4::wave_c();
-
-  v4::KcLoad lq;
-  lq.init(wc * v4::WQ);
-#pragma unroll
-  for (int i = 0; i < v4::LOADS; ++i) {
-    int m = m0 + v4::KcLoad::row_of(i);
-    if (m >= m_end) m = m0;
-    const int qr = a.q_gather ? a.q_gather[m] : m;
-    lq.rowp[i] = (const char*)(a.Q + (size_t)qr * a.q_ld);
-  }
-  v4::KcLoad lp;
-  lp.init(wr * v4::WP);
-#pragma unroll
-  for (int i = 0; i < v4::LOADS; ++i) {
-    const int rr = v4::KcLoad::row_of(i);
-    bool ok;
-    int prow;
-    if (GLU) {
-      prow = glu_prow<C>(rr, rt, a.I, ok);
-    } else {
-      prow = rt * v4::TILE + rr;
-      ok = prow < a.R;
-    }
-    lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
-  }
-
-  f32x16 acc[v4::TI][v4::TJ];
-#pragma unroll
-  for (int ti = 0; ti < v4::TI; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < v4::TJ; ++tj)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
-  __syncthreads();  // s_pref is read; the LDS now belongs to the K loop
-  // Waves whose 64 token rows all lie past the group end (tail tiles) skip their MFMAs.
-  if (m0 + wc * v4::WQ < m_end) v4::mainloop_ring<fp8e4m3, true>(acc, lp, lq, 0, a.K, smem);
-  else v4::mainloop_ring<fp8e4m3, false>(acc, lp, lq, 0, a.K, smem);
-
-  // Epilogue: scales applied in fp32 in registers, then the bf16 results of each wave are staged
-  // in its own LDS block (the ring's final barrier has released the LDS) and stored as whole row
-  // segments: lane (l & 31) of fragment tj is token row q = 32 tj + (l & 31) and holds four
-  // consecutive output channels per 8-channel group g (half h of the lane).
-  const int lane = threadIdx.x & 63;
-  const int h = lane >> 5;
-  const int w = threadIdx.x >> 6;
-  const float* ps = a.p_scale + (size_t)e * a.ps_e;
-  float qsv[v4::TJ];
-#pragma unroll
-  for (int tj = 0; tj < v4::TJ; ++tj) {
-    const int m = m0 + wc * v4::WQ + tj * 32 + (lane & 31);
-    qsv[tj] = m < m_end ? a.q_scale[a.q_gather ? a.q_gather[m] : m] : 0.f;
-  }
-  const int row0 = m0 + wc * v4::WQ;
-  if constexpr (GLU) {
-    // inter block of the wave: 64 token rows x 64 channels (128 bytes), 16-byte chunk c of row
-    // q at c ^ (q & 7).
-    char* wl = smem + w * (v4::WQ * 128);
-#pragma unroll
-    for (int ti = 0; ti < v4::TI / 2; ++ti)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + ti * 32 + 8 * g + 4 * h;
-        const bool cok = ch < a.I;
-        const f32x4 sg = cok ? *(const f32x4*)(ps + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
-        const f32x4 su = cok ? *(const f32x4*)(ps + a.I + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int tj = 0; tj < v4::TJ; ++tj) {
-          float iv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float gv = acc[ti][tj][4 * g + j] * qsv[tj] * sg[j];
-            const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qsv[tj] * su[j];
-            iv[j] = silu(gv) * uv;
-          }
-          const int q = tj * 32 + (lane & 31);
-          const uint2 v = {v2::pack2<bf16>(iv[0], iv[1]), v2::pack2<bf16>(iv[2], iv[3])};
-          *(uint2*)(wl + q * 128 + (((4 * ti + g) ^ (q & 7)) << 4) + 8 * h) = v;
-        }
+  struct Tile { int e, m0, m_end, rt; };
+  auto find = [&](int j, Tile& t) {
+    for (; j < t_cnt; j += nwg) {
+      int mt, rt;
+      v4::tile_of(t_lo + j, a.n_rtiles, mt, rt);
+      if (mt < ex.n_mt) {
+        ex.lookup(mt, t.e, t.m0, t.m_end);
+        t.rt = rt;
+        return j;
       }
-    __syncthreads();
-    const int c = lane & 7;
-    const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + 8 * c;
-#pragma unroll 4
-    for (int it = 0; it < v4::WQ / 8; ++it) {
-      const int q = it * 8 + (lane >> 3);
-      const i32x4 v = *(const i32x4*)(wl + q * 128 + ((c ^ (q & 7)) << 4));
-      if (row0 + q < m_end && ch < a.I) v2::st_stream(v, a.out + (size_t)(row0 + q) * a.I + ch);
     }
-  } else {
+    return t_cnt;
+  };
+  v4::KcLoad lq, lp;
+  auto setup = [&](const Tile& t) {
+    const fp8e4m3* Pe = a.P + (size_t)t.e * a.p_e;
+    lq.init(wc * v4::WQ);
+#pragma unroll
+    for (int i = 0; i < v4::LOADS; ++i) {
+      int m = t.m0 + v4::KcLoad::row_of(i);
+      if (m >= t.m_end) m = t.m0;
+      const int qr = a.q_gather ? a.q_gather[m] : m;
+      lq.rowp[i] = (const char*)(a.Q + (size_t)qr * a.q_ld);
+    }
+    lp.init(wr * v4::WP);
+#pragma unroll
+    for (int i = 0; i < v4::LOADS; ++i) {
+      const int rr = v4::KcLoad::row_of(i);
+      bool ok;
+      int prow;
+      if (GLU) {
+        prow = glu_prow<C>(rr, t.rt, a.I, ok);
+      } else {
+        prow = t.rt * v4::TILE + rr;
+        ok = prow < a.R;
+      }
+      lp.rowp[i] = (const char*)(Pe + (size_t)(ok ? prow : 0) * a.p_ld);
+    }
+  };
+
+  Tile cur;
+  int jt = find(bi, cur);
+  if (jt >= t_cnt) return;
+  setup(cur);
+  v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
+  while (true) {
+    const int e = cur.e, m0 = cur.m0, m_end = cur.m_end, rt = cur.rt;
+    f32x16 acc[v4::TI][v4::TJ];
 #pragma unroll
     for (int ti = 0; ti < v4::TI; ++ti)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int r = rt * v4::TILE + wr * v4::WP + ti * 32 + 8 * g + 4 * h;
-        const f32x4 sr = r < a.R ? *(const f32x4*)(ps + r) : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
-        for (int tj = 0; tj < v4::TJ; ++tj)
+        for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
+    // Waves whose 64 token rows all lie past the group end (tail tiles) skip their MFMAs.
+    if (m0 + wc * v4::WQ < m_end) v4::mainloop_ring<fp8e4m3, true, true>(acc, lp, lq, 0, a.K, smem);
+    else v4::mainloop_ring<fp8e4m3, false, true>(acc, lp, lq, 0, a.K, smem);
+    {
+    // Epilogue: scales applied in fp32 in registers, then the bf16 results of each wave are staged
+    // in its own LDS block (the ring's final barrier has released the LDS) and stored as whole row
+    // segments: lane (l & 31) of fragment tj is token row q = 32 tj + (l & 31) and holds four
+    // consecutive output channels per 8-channel group g (half h of the lane).
+    const int lane = threadIdx.x & 63;
+    const int h = lane >> 5;
+    const int w = threadIdx.x >> 6;
+    const float* ps = a.p_scale + (size_t)e * a.ps_e;
+    float qsv[v4::TJ];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[ti][tj][4 * g + j] *= qsv[tj] * sr[j];
+    for (int tj = 0; tj < v4::TJ; ++tj) {
+      const int m = m0 + wc * v4::WQ + tj * 32 + (lane & 31);
+      qsv[tj] = m < m_end ? a.q_scale[a.q_gather ? a.q_gather[m] : m] : 0.f;
+    }
+    const int row0 = m0 + wc * v4::WQ;
+    if constexpr (GLU) {
+      // inter block of the wave: 64 token rows x 64 channels (128 bytes), 16-byte chunk c of row
+      // q at c ^ (q & 7).
+      char* wl = smem + w * (v4::WQ * 128);
+#pragma unroll
+      for (int ti = 0; ti < v4::TI / 2; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + ti * 32 + 8 * g + 4 * h;
+          const bool cok = ch < a.I;
+          const f32x4 sg = cok ? *(const f32x4*)(ps + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
+          const f32x4 su = cok ? *(const f32x4*)(ps + a.I + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int tj = 0; tj < v4::TJ; ++tj) {
+            float iv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float gv = acc[ti][tj][4 * g + j] * qsv[tj] * sg[j];
+              const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qsv[tj] * su[j];
+              iv[j] = silu(gv) * uv;
+            }
+            const int q = tj * 32 + (lane & 31);
+            const uint2 v = {v2::pack2<bf16>(iv[0], iv[1]), v2::pack2<bf16>(iv[2], iv[3])};
+            *(uint2*)(wl + q * 128 + (((4 * ti + g) ^ (q & 7)) << 4) + 8 * h) = v;
+          }
+        }
+      __syncthreads();
+      const int c = lane & 7;
+      const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + 8 * c;
+#pragma unroll 4
+      for (int it = 0; it < v4::WQ / 8; ++it) {
+        const int q = it * 8 + (lane >> 3);
+        const i32x4 v = *(const i32x4*)(wl + q * 128 + ((c ^ (q & 7)) << 4));
+        if (row0 + q < m_end && ch < a.I) v2::st_stream(v, a.out + (size_t)(row0 + q) * a.I + ch);
       }
-    char* wl = smem + w * (v4::WQ * v2::EPI_ROWB);
-    v2::stage_acc<bf16, v4::TJ>(acc, wl);
-    __syncthreads();
-    v2::store_staged<bf16, v4::WQ>(wl, a.out, a.out_ld, row0, m_end, rt * v4::TILE + wr * v4::WP, a.R);
+    } else {
+#pragma unroll
+      for (int ti = 0; ti < v4::TI; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = rt * v4::TILE + wr * v4::WP + ti * 32 + 8 * g + 4 * h;
+          const f32x4 sr = r < a.R ? *(const f32x4*)(ps + r) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int tj = 0; tj < v4::TJ; ++tj)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[ti][tj][4 * g + j] *= qsv[tj] * sr[j];
+        }
+      char* wl = smem + w * (v4::WQ * v2::EPI_ROWB);
+      v2::stage_acc<bf16, v4::TJ>(acc, wl);
+      __syncthreads();
+      v2::store_staged<bf16, v4::WQ>(wl, a.out, a.out_ld, row0, m_end, rt * v4::TILE + wr * v4::WP, a.R);
+    }
+
+    }
+    Tile nxt;
+    const int jn = find(jt + nwg, nxt);
+    if (jn >= t_cnt) break;
+    setup(nxt);
+    v4::bare_barrier();  // every wave is done with its staging block
+    v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
+    cur = nxt;
+    jt = jn;
   }
 }
 
@@ -203,8 +230,11 @@ static int launch_fp8(Fp8Args a, int64_t n_rows, hipStream_t s) {
   const int64_t max_mt = (n_rows + v2::TILE - 1) / v2::TILE + a.E_glu;
   const int64_t logical = v4::logical_tiles(max_mt, a.n_rtiles);
   if (logical <= 0) return MOE_OK;
-  const int64_t grid = (logical + 7) / 8 * 8;
-  if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+    return MOE_ERR_LAUNCH;
+  const int64_t grid = 8 * std::min<int64_t>(cus / 8, (logical + 7) / 8);
   auto kern = fp8_gemm_kernel<GLU>;
   (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a);

@@ -824,51 +824,6 @@ constexpr int BASE = 1;            // ring slot of each tile's P0
 constexpr int STAGE_B = 4096;      // per-wave staging: 16 rows x 256 bytes
 static_assert(v4::NW * STAGE_B == v4::SLOTB, "the staging of all waves is ring slot 0");
 
-// Expert lookup of token tiles from the sorted-row offsets, in scalar registers: a walk over the
-// experts that resumes where the previous lookup stopped (a workgroup's token tiles come in
-// non-decreasing order when its tile stride is a multiple of the tile group; otherwise the walk
-// restarts). The offsets are read with scalar loads (scalar cache, counted apart from the vector
-// memory operations whose waits the ring relies on).
-struct Experts {
-  const int32_t* off;
-  int E;
-  int n_mt;     // token tiles in total
-  int e, pref;  // walk state: expert e and the index of its first token tile
-  __device__ __forceinline__ void init(const int32_t* offsets, int n_experts) {
-    off = offsets;
-    E = n_experts;
-    const int l = v4::lane_id();
-    int tot = 0;
-    for (int base = 0; base < E; base += 64) {
-      const int x = base + l;
-      int c = x < E ? (offsets[x + 1] - offsets[x] + v4::TILE - 1) / v4::TILE : 0;
-#pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) c += __shfl_xor(c, d, 64);
-      tot += c;
-    }
-    n_mt = __builtin_amdgcn_readfirstlane(tot);
-    e = 0;
-    pref = 0;
-  }
-  // Expert of token tile mt (< n_mt) and its rows [m0, m_end).
-  __device__ __forceinline__ void lookup(int mt, int& ex, int& m0, int& m_end) {
-    if (mt < pref) {
-      e = 0;
-      pref = 0;
-    }
-    int o0 = v3::sload(off + e), o1 = v3::sload(off + e + 1);
-    while (mt >= pref + (o1 - o0 + v4::TILE - 1) / v4::TILE) {
-      pref += (o1 - o0 + v4::TILE - 1) / v4::TILE;
-      ++e;
-      o0 = o1;
-      o1 = v3::sload(off + e + 1);
-    }
-    ex = e;
-    m0 = o0 + (mt - pref) * v4::TILE;
-    m_end = o1;
-  }
-};
-
 struct Tile {
   int e, m0, m_end, rt;
 };
@@ -1008,7 +963,7 @@ token_gemm_v5_kernel(TokenArgs a) {
   using LP = std::conditional_t<P_RC, v4::RcLoad<false, V4Sh16::TI, V4Sh16::FR>, typename V4Sh16::Kc>;
   constexpr bool WGATE = EPI == EPI_GLU_BWD_GATED || EPI == EPI_GLU_FWD;
   extern __shared__ __attribute__((aligned(1024))) char smem[];
-  v5::Experts ex;
+  v4::Experts ex;
   ex.init(a.offsets, a.E_glu);
   const int gm = v4::tile_group(a.n_rtiles);
   const int n_idx = (ex.n_mt + gm - 1) / gm * gm * a.n_rtiles;

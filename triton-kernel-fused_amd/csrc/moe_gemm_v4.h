@@ -429,6 +429,51 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   bare_barrier();
 }
 
+// Expert lookup of token tiles from the sorted-row offsets, in scalar registers: a walk over the
+// experts that resumes where the previous lookup stopped (a workgroup's token tiles come in
+// non-decreasing order when its tile stride is a multiple of the tile group; otherwise the walk
+// restarts). The offsets are read with scalar loads (scalar cache, counted apart from the vector
+// memory operations whose waits the ring relies on).
+struct Experts {
+  const int32_t* off;
+  int E;
+  int n_mt;     // token tiles in total
+  int e, pref;  // walk state: expert e and the index of its first token tile
+  __device__ __forceinline__ void init(const int32_t* offsets, int n_experts) {
+    off = offsets;
+    E = n_experts;
+    const int l = lane_id();
+    int tot = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int x = base + l;
+      int c = x < E ? (offsets[x + 1] - offsets[x] + TILE - 1) / TILE : 0;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) c += __shfl_xor(c, d, 64);
+      tot += c;
+    }
+    n_mt = __builtin_amdgcn_readfirstlane(tot);
+    e = 0;
+    pref = 0;
+  }
+  // Expert of token tile mt (< n_mt) and its rows [m0, m_end).
+  __device__ __forceinline__ void lookup(int mt, int& ex, int& m0, int& m_end) {
+    if (mt < pref) {
+      e = 0;
+      pref = 0;
+    }
+    int o0 = v3::sload(off + e), o1 = v3::sload(off + e + 1);
+    while (mt >= pref + (o1 - o0 + TILE - 1) / TILE) {
+      pref += (o1 - o0 + TILE - 1) / TILE;
+      ++e;
+      o0 = o1;
+      o1 = v3::sload(off + e + 1);
+    }
+    ex = e;
+    m0 = o0 + (mt - pref) * TILE;
+    m_end = o1;
+  }
+};
+
 // Logical tile -> (token tile mt, weight tile rt) of a token GEMM. Up to 8 weight tiles: row-major
 // (rt fastest), so the 32 workgroups an XCD runs at once (32 consecutive logical tiles) cover 4+
 // token tiles x every weight tile. More weight tiles: groups of TGM token tiles with the token tile
