@@ -1095,6 +1095,8 @@ template <typename T, bool RG, bool CG>
 __global__ void __launch_bounds__(v4::NT, 1)
 wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int xr, int xc) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
+  constexpr int PH = 4 + (RG ? 2 : 0) + (CG ? 1 : 0);
+  MOE_PHASE(PH, 0);
   // `order` puts the largest experts first and each expert's tiles are spread over all 8 XCDs
   // (workgroups are dealt to XCDs round-robin, so tile j of an expert runs on XCD j % 8 when the
   // tile count is a multiple of 8). With xr > 0 the r x c tile grid is cut into 8 rectangles of
@@ -1135,8 +1137,14 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
 
   typename V4Sh32::Acc acc[V4Sh32::TI][V4Sh32::TJ];
   V4Sh32::zero(acc);
+  MOE_PHASE(PH, 1);
   v4::mainloop_ring<T>(acc, lp, lq, k0, k1, smem);
+  MOE_PHASE(PH, 2);
   wgrad_epilogue_v2<T, v4::WQ>(acc, a, e, r0, c0, smem, wr, wc);
+#ifdef MOE_PHASE_TRACE
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+  MOE_PHASE(PH, 3);
 }
 
 // dX GEMMs (weights row-contiguous): the five-stage pipeline of moe_gemm_v3.h.
