@@ -194,6 +194,46 @@ def run_router(steps, warmup):
             "workload": f"router epilogue fwd+bwd, fp32 logits N={n} E={e} top-{k}, sigmoid, bias, norm"}
 
 
+def run_vendor_dense(config, steps, warmup):
+    """Context, not a product path: the six GEMMs of one fwd+bwd step of `config` as DENSE bf16
+    torch.matmul calls (hipBLASLt) on the same shapes (M = N*k rows: 2*M*H*2I, 2*M*I*H, 2*M*H*I,
+    2*M*I*H, 2*M*2I*H, 2*M*2I*H FLOP), with no grouping, gather, routing or fused epilogue: the
+    vendor library's rate for the layer's FLOPs on this chip."""
+    import torch
+    from kernels.workloads import CONFIGS
+    c = CONFIGS[config]
+    m, h, i = c["N"] * c["k"], c["H"], c["I"]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=g, dtype=torch.bfloat16)
+    x, wgu, wd = r(m, h), r(2 * i, h), r(h, i)
+    gu, inter, go, ggu = r(m, 2 * i), r(m, i), r(m, h), r(m, 2 * i)
+    gemms = [("gateup_fwd", lambda: x @ wgu.t()), ("down_fwd", lambda: inter @ wd.t()),
+             ("down_dx", lambda: go @ wd), ("wgrad_down", lambda: go.t() @ inter),
+             ("wgrad_gateup", lambda: ggu.t() @ x), ("gateup_dx", lambda: ggu @ wgu)]
+    out = {}
+    total_ms = 0.0
+    for name, fn in gemms:
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        total_ms += ms
+        out[name] = round(ms, 4)
+    f = 18 * m * h * i
+    return {"tflops": round(f / (total_ms * 1e-3) / 1e12, 1), "ms_sum": round(total_ms, 4),
+            "frac_of_peak": round(f / (total_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "gemm_ms": out,
+            "what": (f"dense torch.matmul (hipBLASLt) bf16 on config {config}'s six GEMM shapes "
+                     f"(M={m}, H={h}, I={i}); context for the grouped kernels, not a path of "
+                     f"this library")}
+
+
 def cpu_baseline(config, sample_tokens, reps=3):
     """The oracle's fp32 eager MoE fwd+bwd (a restatement of the reference moe_eager, PyTorch on
     the host cores), on the first `sample_tokens` tokens of the same workload."""
@@ -364,6 +404,8 @@ def main():
                 "frac_of_peak": round(r3["tflops"] / PEAK_BF16_TFLOPS, 4),
                 "routing": dict(router=router, **routing_stats(3, router))}
         line["extra_configs"]["many_experts_zipf_routing"] = routing_stats(3)
+        _log("extra: vendor dense GEMM reference")
+        line["extra_configs"]["vendor_dense_gemm"] = run_vendor_dense(args.config, 10, 3)
         _log("extra: router epilogue")
         line["extra_configs"]["router_epilogue"] = run_router(max(10, args.steps), 3)
     if not args.no_cpu:
