@@ -1065,7 +1065,11 @@ token_gemm_v5_kernel(TokenArgs a) {
     if constexpr (WGATE) {
       if (a.gate) wrow = to_f32(__builtin_bit_cast(T, wbits));
     }
-    MOE_PHASE5(2);
+#ifdef MOE_PHASE_TRACE
+    if (threadIdx.x == 0 && n_tile < 64)  // slot 2: the tile's valid token rows
+      g_phase[((size_t)PH * 65536 + blockIdx.x * 64 + n_tile) * 4 + 2] =
+          (unsigned long long)min(cur.m_end - cur.m0, v4::TILE);
+#endif
     v5::epilogue<T, EPI>(acc, a, cur, wl, wr, wc, wrow);
 #ifdef MOE_PHASE_TRACE
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
