@@ -819,6 +819,13 @@ token_gemm_v4_kernel(TokenArgs a) {
 // token rows at a time through ring slot 0 (4 KB per wave); each tile's ring starts at slot 1.
 // Measured on config 3: gate/up forward -4.7%, down forward -4.3%, gated down dX -1.4%, gate/up
 // dX -1%.
+// 0, opaque to the optimiser (kept in an SGPR).
+__device__ __forceinline__ int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+s"(z));
+  return z;
+}
+
 namespace v5 {
 constexpr int BASE = 1;            // ring slot of each tile's P0
 constexpr int STAGE_B = 4096;      // per-wave staging: 16 rows x 256 bytes
@@ -994,23 +1001,22 @@ token_gemm_v5_kernel(TokenArgs a) {
       if (a.gate) gp = (const unsigned short*)a.gate + (a.sflat ? a.sflat[m] : m);
       wbits = *gp;
     }
-    lq.init(wc * v4::WQ);
+    // (The loaders' lane constants are set once, before the tile loop: recomputed per tile they
+    // were kept twice and spilled.)
 #pragma unroll
     for (int i = 0; i < v4::LOADS; ++i) {
       int m = t.m0 + v4::KcLoad::row_of(i);
       if (m >= t.m_end) m = t.m0;
-      const int qr = a.q_gather ? a.q_gather[m] : m;
+      // The plain-store GEMMs read sorted rows (no gather; checked at launch): no index load,
+      // whose wait would also wait for the previous tile's epilogue stores.
+      const int qr = (EPI != EPI_STORE && a.q_gather) ? a.q_gather[m] : m;
       lq.rowp[i] = (const char*)((const T*)a.Q + (size_t)qr * a.q_ld);
     }
     if constexpr (P_RC) {
       const int r0 = t.rt * v4::TILE;
       lp.src = (const char*)(Pe + r0);
-      lp.ld = (size_t)a.p_ld * sizeof(T);
-      lp.gather = nullptr;
-      lp.kend = a.K;
-      lp.init(wr * v4::WP, a.R - r0);
+      lp.set_rvalid(a.R - r0);
     } else {
-      lp.init(wr * v4::WP);
 #pragma unroll
       for (int i = 0; i < v4::LOADS; ++i) {
         const int rr = v4::KcLoad::row_of(i);
@@ -1032,9 +1038,18 @@ token_gemm_v5_kernel(TokenArgs a) {
   if (j >= t_cnt) return;
   LP lp;
   LQ lq;
+  lq.init(wc * v4::WQ);
+  if constexpr (P_RC) {
+    lp.ld = (size_t)a.p_ld * sizeof(T);
+    lp.gather = nullptr;
+    lp.kend = a.K;
+    lp.init(wr * v4::WP, a.R);
+  } else {
+    lp.init(wr * v4::WP);
+  }
   unsigned short wbits = 0;
   setup(cur, lp, lq, wbits);
-  v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
+  v4::ring_prologue<T>(lp, lq, opaque_zero(), a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
   char* wl = smem + (threadIdx.x >> 6) * v5::STAGE_B;  // staging: ring slot 0
 #ifdef MOE_PHASE_TRACE
   constexpr int PH = 8 + EPI * 2 + (P_RC ? 1 : 0);
@@ -1049,13 +1064,17 @@ token_gemm_v5_kernel(TokenArgs a) {
 #endif
   while (true) {
     MOE_PHASE5(0);
-    v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, v4::NSLOT - 1, 1);  // P2 -> slot 0
+    // K starts at 0 for every tile, but as a value the compiler cannot see: otherwise it computes
+    // the prologue's row and address terms once, keeps them live across the tile loop and spills
+    // them, and each reload's wait then drains the ring loads already in flight.
+    const int kz = opaque_zero();
+    v4::ring_prologue<T>(lp, lq, kz, a.K, smem, v5::BASE, v4::NSLOT - 1, 1);  // P2 -> slot 0
     typename V4Sh16::Acc acc[V4Sh16::TI][V4Sh16::TJ];
     V4Sh16::zero(acc);
     if (cur.m0 + wc * v4::WQ < cur.m_end)
-      v4::mainloop_ring<T, true, true>(acc, lp, lq, 0, a.K, smem, v5::BASE);
+      v4::mainloop_ring<T, true, true>(acc, lp, lq, kz, a.K, smem, v5::BASE);
     else
-      v4::mainloop_ring<T, false, true>(acc, lp, lq, 0, a.K, smem, v5::BASE);
+      v4::mainloop_ring<T, false, true>(acc, lp, lq, kz, a.K, smem, v5::BASE);
     // The ring is drained and every wave is past its last read: slots 1-4 take the next tile's
     // first loads while this tile's epilogue stages through slot 0.
     MOE_PHASE5(1);
@@ -1085,7 +1104,7 @@ token_gemm_v5_kernel(TokenArgs a) {
     // for the last tile too (on valid, unused values): unconditional, it keeps the register
     // allocation free of spills.
     setup(jn < t_cnt ? nxt : cur, lp, lq, wbits);
-    if (jn < t_cnt) v4::ring_prologue<T>(lp, lq, 0, a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
+    if (jn < t_cnt) v4::ring_prologue<T>(lp, lq, opaque_zero(), a.K, smem, v5::BASE, 0, v4::NSLOT - 1);
     if (jn >= t_cnt) break;
     v4::bare_barrier();  // every wave is done with slot 0 before P2 lands in it
     cur = nxt;
@@ -1278,7 +1297,7 @@ static int launch_token_v2(TokenArgs a, int64_t n_rows, hipStream_t s) {
   const bool split = EPI == EPI_STORE && a.split_ws && a.K / 64 >= v4::SPLIT_MIN_STEPS;
   const int cus = device_cus();
   if constexpr (EPI != EPI_GLU_BWD) {
-  if (a.K % 64 == 0 && !split && cus >= 8) {
+  if (a.K % 64 == 0 && !split && cus >= 8 && (EPI != EPI_STORE || !a.q_gather)) {
     const int64_t per_xcd = (logical + 7) / 8;
     const int64_t grid = 8 * std::min<int64_t>(cus / 8, per_xcd);
     auto kern = token_gemm_v5_kernel<T, EPI, P_RC>;

@@ -151,6 +151,17 @@ struct RcLoad {
                   ((((rbase >> 3) + 2 * t + (p >> 1)) ^ (4 * q) ^ (2 * (l >> 4))) * 16) + 8 * (p & 1);
     }
   }
+  // The column clamp of a new r range (rvalid columns inside the operand); the rest of init()
+  // depends only on the lane and rbase.
+  __device__ __forceinline__ void set_rvalid(int rvalid) {
+    const int l = lane_id(), h = l >> 5;
+    const int wx = FR == 16 ? 2 * (wave_id() & 3) : 0;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int c = (l & 31) ^ (4 * ((2 * par + h) & 3)) ^ wx;
+      cbyte[par] = min(8 * c, rvalid - 8) * 2;
+    }
+  }
   __device__ __forceinline__ void fetch_rows(int k) {
     if constexpr (GATHER) {
       const int kw = k + wave_id() * 2 * LOADS;
