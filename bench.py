@@ -234,6 +234,45 @@ def run_vendor_dense(config, steps, warmup):
                      f"this library")}
 
 
+def run_vendor_dense_fp8(steps, warmup):
+    """Context, not a product path: config 4's two forward GEMMs as DENSE fp8-e4m3
+    torch._scaled_mm calls (hipBLASLt) with per-row x per-column fp32 scales and bf16 output, on
+    the same shapes (M = N*k rows: 2*M*H*2I and 2*M*I*H FLOP), no grouping, gather or SwiGLU."""
+    import torch
+    from kernels.workloads import CONFIGS
+    c = CONFIGS[4]
+    m, h, i = c["N"] * c["k"], c["H"], c["I"]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    f8 = torch.float8_e4m3fn
+    r = lambda *sh: torch.randn(*sh, device="cuda", generator=g).to(f8)
+    x, wgu, inter, wd = r(m, h), r(2 * i, h), r(m, i), r(h, i)
+    sx, si = torch.rand(m, 1, device="cuda") + 0.5, torch.rand(m, 1, device="cuda") + 0.5
+    sgu, sd = torch.rand(1, 2 * i, device="cuda") + 0.5, torch.rand(1, h, device="cuda") + 0.5
+    gemms = [("gateup", lambda: torch._scaled_mm(x, wgu.t(), sx, sgu, out_dtype=torch.bfloat16)),
+             ("down", lambda: torch._scaled_mm(inter, wd.t(), si, sd, out_dtype=torch.bfloat16))]
+    out, total_ms = {}, 0.0
+    for name, fn in gemms:
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        total_ms += ms
+        out[name] = round(ms, 4)
+    f = 6 * m * h * i
+    return {"tflops": round(f / (total_ms * 1e-3) / 1e12, 1), "ms_sum": round(total_ms, 4),
+            "frac_of_peak": round(f / (total_ms * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "gemm_ms": out,
+            "what": (f"dense torch._scaled_mm (hipBLASLt) fp8-e4m3 with row/column scales on config "
+                     f"4's two forward GEMM shapes (M={m}, H={h}, I={i}); context, not a path of "
+                     f"this library")}
+
+
 def cpu_baseline(config, sample_tokens, reps=3):
     """The oracle's fp32 eager MoE fwd+bwd (a restatement of the reference moe_eager, PyTorch on
     the host cores), on the first `sample_tokens` tokens of the same workload."""
@@ -406,6 +445,10 @@ def main():
         line["extra_configs"]["many_experts_zipf_routing"] = routing_stats(3)
         _log("extra: vendor dense GEMM reference")
         line["extra_configs"]["vendor_dense_gemm"] = run_vendor_dense(args.config, 10, 3)
+        try:
+            line["extra_configs"]["vendor_dense_gemm_fp8"] = run_vendor_dense_fp8(10, 3)
+        except (RuntimeError, TypeError) as exc:  # a torch build without row-wise fp8 scaling
+            line["extra_configs"]["vendor_dense_gemm_fp8"] = {"error": str(exc)[:200]}
         _log("extra: router epilogue")
         line["extra_configs"]["router_epilogue"] = run_router(max(10, args.steps), 3)
     if not args.no_cpu:
