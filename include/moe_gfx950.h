@@ -222,14 +222,19 @@ int moe_glu_bwd(int dtype, const void* grad_out, int64_t go_row_stride, int64_t 
  * fp8 path — the algorithm is the bf16 pipeline of moe_grouped_gateup_swiglu_fwd /
  * moe_grouped_down_fwd with quantised operands). x_q (N,H) e4m3 + x_scale (N) fp32 (per token);
  * w13_q (E,2I,H) e4m3 + w13_scale (E,2I) fp32 and w2_q (E,H,I) + w2_scale (E,H) fp32 (per
- * output channel). Writes inter (M,I) bf16 = SiLU(gate)*up, inter_q (M,I) e4m3 + inter_scale (M)
- * (per routed row, absmax/448) and eo (M,H) bf16; moe_combine_fwd (bf16) makes the output.
+ * output channel). Writes inter_q (M,I) e4m3 = SiLU(gate)*up re-quantised with one E8M0 scale
+ * per routed row and 128-channel block (the smallest power of two 2^e with 448 * 2^e >= the
+ * block's absmax), those scales into inter_bscale (a table of moe_fp8_inter_bscale_bytes bytes,
+ * layout private to the library), and eo (M,H) bf16; moe_combine_fwd (bf16) makes the output.
  * H and I must be multiples of 128. */
 int moe_fp8_fwd(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t H,
                 const void* w13_q, const float* w13_scale, const void* w2_q, const float* w2_scale,
                 int E, int64_t I, const int32_t* offsets, const int32_t* sorted_token,
-                int64_t n_rows, void* inter, void* inter_q, float* inter_scale, void* eo,
-                void* stream);
+                int64_t n_rows, void* inter_q, void* inter_bscale, void* eo, void* stream);
+
+/* Bytes of moe_fp8_fwd's inter_bscale for I, n_rows routed rows and E experts (0 for invalid
+ * sizes). No counterpart in the reference. */
+int64_t moe_fp8_inter_bscale_bytes(int64_t I, int64_t n_rows, int E);
 
 /* Per-row absmax fp8 quantisation: scale[m] = absmax(x[m,:]) / 448 (1 for a zero row),
  * q = e4m3(x / scale), round to nearest even. x (n_rows, K) bf16, K a multiple of 8. */

@@ -211,13 +211,30 @@ def e4m3_round(x):
     return x.clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn).to(x.dtype)
 
 
+def e8m0_block_requant(y, block):
+    """Re-quantise the rows of y to e4m3 with one power-of-two scale per `block` consecutive
+    values: 2^e with e the smallest integer for which 448 * 2^e >= the block's absmax (so no value
+    saturates; e = -127 for an all-zero block, and e >= -127 always, the E8M0 range). Returns the
+    dequantised values and the E8M0 codes e + 127 of shape (rows, cols / block)."""
+    n, k = y.shape
+    yb = y.reshape(n, k // block, block)
+    amax = yb.abs().amax(-1)
+    m, ex = torch.frexp(amax)                      # amax = m * 2^ex, m in [0.5, 1); 448 = 0.875 * 2^9
+    e = ex - 9 + (m > 0.875).to(ex.dtype)
+    e = torch.where(amax > 0, e, torch.full_like(e, -127)).clamp(min=-127)
+    sc = torch.exp2(e.to(y.dtype)).unsqueeze(-1)
+    return (e4m3_round(yb / sc) * sc).reshape(n, k), e + 127
+
+
 def fp8_forward(x_q, x_scale, idx, wt, gate_up_q, gate_up_scale, down_q, down_scale,
-                requant_inter=True, inter_bf16=False, dtype=torch.float32):
+                requant_inter=True, inter_bf16=False, requant_block=128, dtype=torch.float32):
     """fp8 MoE forward in fp32 from quantised operands.
     gate_up = (x_q . W_q^T) * x_scale[t] * w_scale[n]; inter = SiLU(gate)*up (rounded to bf16 first
-    when inter_bf16, as a kernel that stores it in bf16 does), re-quantised per row (absmax/448)
-    when requant_inter; eo = (inter_q . Wd_q^T) * inter_scale * wd_scale[h];
-    out[t] = sum_j w[t,j] * eo, all in `dtype` (fp32 by default). Returns (N,H) in `dtype`."""
+    when inter_bf16), re-quantised to e4m3 when requant_inter: with requant_block > 0 one
+    power-of-two scale per block of that many channels of a routed row (e8m0_block_requant, what
+    the gfx950 kernels do with 128), with requant_block = 0 one scale per row (absmax/448);
+    eo = inter_q . Wd^T * wd_scale[h]; out[t] = sum_j w[t,j] * eo, all in `dtype` (fp32 by default).
+    Returns (N,H) in `dtype`."""
     n, h = x_q.shape
     inter = gate_up_q.shape[1] // 2
     xf = x_q.to(dtype)
@@ -233,7 +250,9 @@ def fp8_forward(x_q, x_scale, idx, wt, gate_up_q, gate_up_scale, down_q, down_sc
         y = F.silu(gu[:, :inter]) * gu[:, inter:]
         if inter_bf16:
             y = y.bfloat16().to(dtype)
-        if requant_inter:
+        if requant_inter and requant_block > 0:
+            y = e8m0_block_requant(y, requant_block)[0]
+        elif requant_inter:
             amax = y.abs().amax(-1, keepdim=True)
             s = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
             y = e4m3_round(y / s) * s

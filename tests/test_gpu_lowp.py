@@ -1,9 +1,10 @@
 """GPU parity of the quantised forwards (fp8-e4m3, MXFP8) against the fp32 dequantised oracle.
 
 Tolerance (north star): relative Frobenius error ||ours - ref|| / ||ref|| <= 3e-2, ref computed in
-fp32 from the same quantised operands (oracle.fp8_forward re-quantises the SwiGLU intermediate per
-routed row exactly as the kernel does; oracle.mxfp8_forward dequantises the E8M0-scaled weights).
-The row quantiser must agree bit for bit with torch's float8_e4m3fn conversion.
+fp32 from the same quantised operands (oracle.fp8_forward re-quantises the SwiGLU intermediate
+with one power-of-two scale per routed row and 128-channel block, as the kernel does;
+oracle.mxfp8_forward dequantises the E8M0-scaled weights). The row quantiser must agree bit for
+bit with torch's float8_e4m3fn conversion.
 """
 import pytest
 import torch
@@ -48,8 +49,8 @@ def _fp8_args(w):
 def test_fp8_small_vs_oracle(scale):
     w = make_workload(4, scale=scale)
     _say(f"fp8 {scale}")
-    ref = orc.fp8_forward(*_fp8_args(w))
-    alg = orc.fp8_forward(*_fp8_args(w), inter_bf16=True)
+    ref = orc.fp8_forward(*_fp8_args(w), requant_inter=False)
+    alg = orc.fp8_forward(*_fp8_args(w))
     out = kernels.moe_fp8(*[t.cuda() for t in _fp8_args(w)]).cpu()
     err = _frob(out, ref)
     assert err <= 3e-2, err                     # the spec: fp32 dequantised reference
@@ -64,8 +65,10 @@ def test_fp8_config4_full_vs_oracle_on_gpu():
     ref = orc.fp8_forward(*_fp8_args(w))
     err = _frob(out, ref)
     ref_nq = orc.fp8_forward(*_fp8_args(w), requant_inter=False)
-    print(f"fp8 config 4: frob vs requant oracle {err:.3e}, vs fp32 intermediate {_frob(out, ref_nq):.3e}")
-    assert err <= 3e-2, err
+    err_nq = _frob(out, ref_nq)
+    print(f"fp8 config 4: frob vs requant oracle {err:.3e}, vs fp32 intermediate {err_nq:.3e}")
+    assert err <= 3e-3, err
+    assert err_nq <= 3e-2, err_nq
 
 
 @pytest.mark.parametrize("scale", [dict(N=64, H=512, I=512, E=16, k=8),

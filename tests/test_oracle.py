@@ -176,13 +176,14 @@ def test_mxfp8_quantiser():
 
 
 def test_fp8_forward_requant_only_differs_by_intermediate():
-    w = make_workload(4, scale=dict(N=64, H=64, I=64, E=4, k=2))
+    w = make_workload(4, scale=dict(N=64, H=64, I=128, E=4, k=2))
     args = (w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"],
             w["down_q"], w["down_scale"])
-    a = orc.fp8_forward(*args, requant_inter=True)
     b = orc.fp8_forward(*args, requant_inter=False)
-    rel = ((a - b).norm() / b.norm()).item()
-    assert 1e-4 < rel < 5e-2
+    for blk in (0, 128, 32):
+        a = orc.fp8_forward(*args, requant_inter=True, requant_block=blk)
+        rel = ((a - b).norm() / b.norm()).item()
+        assert 1e-4 < rel < 5e-2, (blk, rel)
 
 
 # ── independent pins of the fp8 / MXFP8 forwards ──
@@ -249,7 +250,7 @@ def test_fp8_forward_with_requant_matches_scalar_loops():
     w = _tiny_fp8_case(seed=3)
     got = orc.fp8_forward(w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"],
                           w["gate_up_scale"], w["down_q"], w["down_scale"], requant_inter=True,
-                          dtype=torch.float64)
+                          requant_block=0, dtype=torch.float64)
     xq, xs = w["x_q"].double().tolist(), w["x_scale"].double().tolist()
     gq, gs = w["gate_up_q"].double().tolist(), w["gate_up_scale"].double().tolist()
     dq, ds = w["down_q"].double().tolist(), w["down_scale"].double().tolist()
@@ -264,6 +265,54 @@ def test_fp8_forward_with_requant_matches_scalar_loops():
             amax = max(abs(v) for v in y)
             s = amax / 448.0 if amax > 0 else 1.0
             y = [_e4m3_round_loop(v / s) * s for v in y]
+            for r in range(h):
+                ref[t][r] += wt[t][j] * sum(y[c] * dq[e][r][c] for c in range(i)) * ds[e][r]
+    torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=1e-9, atol=1e-9)
+
+
+def _e8m0_exponent_loop(amax):
+    """Smallest integer e >= -127 with 448 * 2^e >= amax, by counting (no logarithms)."""
+    e = -127
+    while 448.0 * 2.0 ** e < amax:
+        e += 1
+    return e
+
+
+def test_e8m0_block_requant_matches_loops():
+    g = torch.Generator().manual_seed(6)
+    y = torch.randn(5, 256, generator=g, dtype=torch.float64) * torch.tensor(
+        [[1e-30], [1e-3], [1.0], [300.0], [1.0]], dtype=torch.float64)
+    y[4, 128:] = 0                                  # an all-zero block
+    y[2, 5] = 448.0                                 # amax exactly 448 * 2^0
+    y[2, 200] = 448.0 * 2 ** -3 * (1 + 2 ** -20)    # just above a power-of-two boundary
+    got, codes = orc.e8m0_block_requant(y, 128)
+    for r in range(5):
+        for b in range(2):
+            blk = y[r, 128 * b:128 * b + 128].tolist()
+            e = _e8m0_exponent_loop(max(abs(v) for v in blk))
+            assert int(codes[r, b]) == e + 127
+            ref = [_e4m3_round_loop(v / 2.0 ** e) * 2.0 ** e for v in blk]
+            assert got[r, 128 * b:128 * b + 128].tolist() == ref
+    assert int(codes[4, 1]) == 0 and int(codes[2, 0]) == 127 and int(codes[2, 1]) == 125
+
+
+def test_fp8_forward_with_block_requant_matches_scalar_loops():
+    w = make_workload(4, seed=7, scale=dict(N=5, H=32, I=128, E=3, k=2))
+    got = orc.fp8_forward(w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"],
+                          w["gate_up_scale"], w["down_q"], w["down_scale"], dtype=torch.float64)
+    xq, xs = w["x_q"].double().tolist(), w["x_scale"].double().tolist()
+    gq, gs = w["gate_up_q"].double().tolist(), w["gate_up_scale"].double().tolist()
+    dq, ds = w["down_q"].double().tolist(), w["down_scale"].double().tolist()
+    idx, wt = w["idx"].tolist(), w["wt"].double().tolist()
+    n, h, i = 5, 32, 128
+    ref = [[0.0] * h for _ in range(n)]
+    for t in range(n):
+        for j, e in enumerate(idx[t]):
+            gu = [sum(xq[t][c] * gq[e][r][c] for c in range(h)) * xs[t] * gs[e][r]
+                  for r in range(2 * i)]
+            y = [gu[c] / (1.0 + math.exp(-gu[c])) * gu[i + c] for c in range(i)]
+            ex = _e8m0_exponent_loop(max(abs(v) for v in y))   # one 128-channel block
+            y = [_e4m3_round_loop(v / 2.0 ** ex) * 2.0 ** ex for v in y]
             for r in range(h):
                 ref[t][r] += wt[t][j] * sum(y[c] * dq[e][r][c] for c in range(i)) * ds[e][r]
     torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=1e-9, atol=1e-9)

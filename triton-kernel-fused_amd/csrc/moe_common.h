@@ -111,6 +111,15 @@ template <> struct Mfma<fp8e4m3> {
     const i32x8 b8 = __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7);
     c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 0, 0, 0, 127, 0, 127);
   }
+  // The same with a per-lane E8M0 scale for B: byte SEL of sb scales the 32 K values the lane
+  // holds (one block of one B column); A unscaled.
+  template <int SEL>
+  __device__ __forceinline__ static void stepf_sb(f32x16& c, const i32x4* a, const i32x4* b,
+                                                  unsigned sb) {
+    const i32x8 a8 = __builtin_shufflevector(a[0], a[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    const i32x8 b8 = __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 0, 0, 0, 127, SEL, (int)sb);
+  }
 };
 
 __device__ __forceinline__ i32x4 ldg16(const void* p) { return *(const i32x4*)p; }

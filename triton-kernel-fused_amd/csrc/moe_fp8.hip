@@ -1,13 +1,15 @@
-// fp8-e4m3 MoE forward (inference): grouped gate/up GEMM with scales + SwiGLU, per-row
-// re-quantisation of the intermediate, grouped down GEMM with scales.
+// fp8-e4m3 MoE forward (inference): grouped gate/up GEMM with scales + SwiGLU + re-quantisation
+// of the intermediate, grouped down GEMM with scales.
 //
-// Operands are OCP e4m3fn with fp32 scales: activations per token, weights per output channel,
-// the intermediate per routed row (absmax / 448). The GEMMs run the eight-wave 256x256 ring
-// pipeline of moe_gemm_v4.h on v_mfma_scale_f32_32x32x64_f8f6f4 with neutral E8M0 scales (the
-// plain fp8 product); the per-token and per-channel scales factor out of the K sum and are applied in the
-// epilogue: y[m, n] = (sum_k xq[m,k] wq[n,k]) * sx[m] * sw[n].
-// The gate/up epilogue cannot quantise the intermediate itself (a row's absmax spans every
-// column tile), so it stores SiLU(gate)*up in bf16 and a row kernel quantises it.
+// Operands are OCP e4m3fn: activations with an fp32 scale per token, weights with an fp32 scale
+// per output channel. The GEMMs run the eight-wave 256x256 ring pipeline of moe_gemm_v4.h on
+// v_mfma_scale_f32_32x32x64_f8f6f4; the fp32 scales factor out of the K sum and are applied in
+// the epilogue: gate_up[m, n] = (sum_k xq[m,k] wq[n,k]) * sx[m] * sw[n].
+// The gate/up epilogue quantises the intermediate itself, one power-of-two (E8M0) scale per
+// token row and 128-channel block: a block is the tile's channel range, so its absmax is known in
+// the epilogue (the two P-half waves exchange theirs through LDS), and a block is one K step of
+// the down GEMM, whose MFMAs take the scales through their B-scale operand (v4::KcLoadS):
+// eo[m, h] = (sum_k 2^e[m, k/128] iq[m,k] wq[h,k]) * sw[h].
 #include "moe_gemm_common.h"
 #include "moe_gemm_v4.h"
 
@@ -22,11 +24,15 @@ struct Fp8Args {
   const fp8e4m3* Q;        // token-side rows, K contiguous
   long long q_ld;
   const int32_t* q_gather; // sorted row -> Q row, or null
-  const float* q_scale;    // per Q row (indexed like Q rows)
+  const float* q_scale;    // GLU: per Q row (indexed like Q rows)
+  const uint8_t* q_bscale; // down: E8M0 block scales of the intermediate (KcLoadS table layout)
+  long long bs_ld;         // scale table row pitch (bytes)
   const int32_t* offsets;
   int E_glu, n_rtiles;
-  bf16* out;               // GLU: inter (M, I); plain: (M, out_ld)
+  bf16* out;               // down: (M, out_ld) bf16
   long long out_ld;
+  fp8e4m3* out_q;          // GLU: intermediate (M, I) e4m3
+  uint8_t* out_bscale;     // GLU: its E8M0 block scales (written in the KcLoadS table layout)
 };
 
 // Persistent: one workgroup per CU slot of an XCD runs the XCD's logical tiles bi, bi + n_wg, ...
@@ -45,7 +51,7 @@ fp8_gemm_kernel(Fp8Args a) {
   const int R8 = (n_idx + 7) >> 3;
   const int t_lo = xcd * R8, t_cnt = max(0, min(n_idx, t_lo + R8) - t_lo);
   const int wr = v4::wave_r(), wc = v4::wave_c();
-  struct Tile { int e, m0, m_end, rt; };
+  struct Tile { int e, m0, m_end, rt, mt; };
   auto find = [&](int j, Tile& t) {
     for (; j < t_cnt; j += nwg) {
       int mt, rt;
@@ -53,15 +59,22 @@ fp8_gemm_kernel(Fp8Args a) {
       if (mt < ex.n_mt) {
         ex.lookup(mt, t.e, t.m0, t.m_end);
         t.rt = rt;
+        t.mt = mt;
         return j;
       }
     }
     return t_cnt;
   };
-  v4::KcLoad lq, lp;
+  std::conditional_t<GLU, v4::KcLoad, v4::KcLoadS> lq;
+  v4::KcLoad lp;
   auto setup = [&](const Tile& t) {
     const fp8e4m3* Pe = a.P + (size_t)t.e * a.p_e;
     lq.init(wc * v4::WQ);
+    if constexpr (!GLU) {
+      lq.sp = (const char*)a.q_bscale + (size_t)t.mt * v4::TILE + wc * v4::WQ +
+              2 * (v4::lane_id() & 31);
+      lq.s_ld = a.bs_ld;
+    }
 #pragma unroll
     for (int i = 0; i < v4::LOADS; ++i) {
       int m = t.m0 + v4::KcLoad::row_of(i);
@@ -88,10 +101,13 @@ fp8_gemm_kernel(Fp8Args a) {
   Tile cur;
   int jt = find(bi, cur);
   if (jt >= t_cnt) return;
+  // The gate/up GEMM issues the next tile's ring loads right after the epilogue; the down GEMM's
+  // K loop issues them itself (its block-scale loads must not be in flight across the tile loop).
+  constexpr bool PRE = GLU;
   setup(cur);
-  v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
+  if (PRE) v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
   while (true) {
-    const int e = cur.e, m0 = cur.m0, m_end = cur.m_end, rt = cur.rt;
+    const int e = cur.e, m0 = cur.m0, m_end = cur.m_end, rt = cur.rt, mt = cur.mt;
     f32x16 acc[v4::TI][v4::TJ];
 #pragma unroll
     for (int ti = 0; ti < v4::TI; ++ti)
@@ -100,8 +116,8 @@ fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[ti][tj][v] = 0.f;
     // Waves whose 64 token rows all lie past the group end (tail tiles) skip their MFMAs.
-    if (m0 + wc * v4::WQ < m_end) v4::mainloop_ring<fp8e4m3, true, true>(acc, lp, lq, 0, a.K, smem);
-    else v4::mainloop_ring<fp8e4m3, false, true>(acc, lp, lq, 0, a.K, smem);
+    if (m0 + wc * v4::WQ < m_end) v4::mainloop_ring<fp8e4m3, true, PRE>(acc, lp, lq, 0, a.K, smem);
+    else v4::mainloop_ring<fp8e4m3, false, PRE>(acc, lp, lq, 0, a.K, smem);
     {
     // Epilogue: scales applied in fp32 in registers, then the bf16 results of each wave are staged
     // in its own LDS block (the ring's final barrier has released the LDS) and stored as whole row
@@ -111,17 +127,18 @@ fp8_gemm_kernel(Fp8Args a) {
     const int h = lane >> 5;
     const int w = threadIdx.x >> 6;
     const float* ps = a.p_scale + (size_t)e * a.ps_e;
-    float qsv[v4::TJ];
-#pragma unroll
-    for (int tj = 0; tj < v4::TJ; ++tj) {
-      const int m = m0 + wc * v4::WQ + tj * 32 + (lane & 31);
-      qsv[tj] = m < m_end ? a.q_scale[a.q_gather ? a.q_gather[m] : m] : 0.f;
-    }
     const int row0 = m0 + wc * v4::WQ;
     if constexpr (GLU) {
-      // inter block of the wave: 64 token rows x 64 channels (128 bytes), 16-byte chunk c of row
-      // q at c ^ (q & 7).
-      char* wl = smem + w * (v4::WQ * 128);
+      float qsv[v4::TJ];
+#pragma unroll
+      for (int tj = 0; tj < v4::TJ; ++tj) {
+        const int m = row0 + tj * 32 + (lane & 31);
+        qsv[tj] = m < m_end ? a.q_scale[a.q_gather ? a.q_gather[m] : m] : 0.f;
+      }
+      // SiLU(gate) * up in fp32, in place of the gate accumulators: lane (l & 31) of fragment tj
+      // is token row q = 32 tj + (l & 31) and holds channels 32 ti + 8 g + 4 h + j of the wave's
+      // 64 (h = l / 32, the partner lane l ^ 32 holds the other half).
+      float am[v4::TJ] = {0.f, 0.f};
 #pragma unroll
       for (int ti = 0; ti < v4::TI / 2; ++ti)
 #pragma unroll
@@ -131,27 +148,75 @@ fp8_gemm_kernel(Fp8Args a) {
           const f32x4 sg = cok ? *(const f32x4*)(ps + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
           const f32x4 su = cok ? *(const f32x4*)(ps + a.I + ch) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int tj = 0; tj < v4::TJ; ++tj) {
-            float iv[4];
+          for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const float gv = acc[ti][tj][4 * g + j] * qsv[tj] * sg[j];
               const float uv = acc[ti + v4::TI / 2][tj][4 * g + j] * qsv[tj] * su[j];
-              iv[j] = silu(gv) * uv;
+              const float iv = silu(gv) * uv;
+              acc[ti][tj][4 * g + j] = iv;
+              am[tj] = fmaxf(am[tj], fabsf(iv));
             }
-            const int q = tj * 32 + (lane & 31);
-            const uint2 v = {v2::pack2<bf16>(iv[0], iv[1]), v2::pack2<bf16>(iv[2], iv[3])};
-            *(uint2*)(wl + q * 128 + (((4 * ti + g) ^ (q & 7)) << 4) + 8 * h) = v;
-          }
         }
+      // Block absmax over the tile's 128 channels of each token row: the partner lane, then the
+      // other P-half wave (same token rows) through LDS (above the 32 KB of staging blocks).
+      float* xam = (float*)(smem + 32768) + wc * (2 * v4::WQ);
+#pragma unroll
+      for (int tj = 0; tj < v4::TJ; ++tj) {
+        am[tj] = fmaxf(am[tj], __shfl_xor(am[tj], 32, 64));
+        if (h == 0) xam[wr * v4::WQ + tj * 32 + lane] = am[tj];
+      }
       __syncthreads();
-      const int c = lane & 7;
-      const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2) + 8 * c;
-#pragma unroll 4
-      for (int it = 0; it < v4::WQ / 8; ++it) {
-        const int q = it * 8 + (lane >> 3);
-        const i32x4 v = *(const i32x4*)(wl + q * 128 + ((c ^ (q & 7)) << 4));
-        if (row0 + q < m_end && ch < a.I) v2::st_stream(v, a.out + (size_t)(row0 + q) * a.I + ch);
+      // E8M0 exponent per token row: the smallest e with 448 * 2^e >= absmax (for absmax =
+      // 1.f * 2^E: e = E - 8, plus one when 1.f > 1.75), clamped to [-127, ...]; byte = e + 127.
+      unsigned code[v4::TJ];
+      float inv[v4::TJ];
+#pragma unroll
+      for (int tj = 0; tj < v4::TJ; ++tj) {
+        const int q = tj * 32 + (lane & 31);
+        const float amax = fmaxf(xam[q], xam[v4::WQ + q]);
+        const unsigned b = __float_as_uint(amax);
+        const int c = (int)(b >> 23) - 8 + ((b & 0x7fffff) > 0x600000u ? 1 : 0);
+        code[tj] = (unsigned)max(c, 0);
+        inv[tj] = __uint_as_float((254u - code[tj]) << 23);  // 2^-e, exact
+      }
+      // e4m3 bytes of the wave's 64 rows x 64 channels, staged per wave as [row q][64 bytes]:
+      // 16-byte chunk c of row q at c ^ ((q >> 2) & 3).
+      char* wl = smem + w * (v4::WQ * 64);
+#pragma unroll
+      for (int ti = 0; ti < v4::TI / 2; ++ti)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int tj = 0; tj < v4::TJ; ++tj) {
+            const f32x16& v = acc[ti][tj];
+            int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g] * inv[tj], v[4 * g + 1] * inv[tj], 0,
+                                                    false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * g + 2] * inv[tj], v[4 * g + 3] * inv[tj], p,
+                                                true);
+            const int q = tj * 32 + (lane & 31);
+            const int chunk = ti * 2 + (g >> 1), pos = 2 * (g & 1) + h;
+            *(int*)(wl + q * 64 + ((chunk ^ ((q >> 2) & 3)) << 4) + 4 * pos) = p;
+          }
+      // Scales: table row rt (the down GEMM's K step), the token tile's 256 bytes, bytes 2j /
+      // 2j+1 of the wave's 64 = its rows j / j+32.
+      if (wr == 0 && h == 0) {
+#pragma unroll
+        for (int tj = 0; tj < v4::TJ; ++tj)
+          if (row0 + tj * 32 + lane < m_end)
+            a.out_bscale[(size_t)rt * a.bs_ld + (size_t)mt * v4::TILE + wc * v4::WQ + 2 * lane + tj] =
+                (uint8_t)code[tj];
+      }
+      __syncthreads();
+      const int c = lane & 3;
+      const int ch = rt * (v4::TILE / 2) + wr * (v4::WP / 2);
+#pragma unroll
+      for (int it = 0; it < v4::WQ / 16; ++it) {
+        const int q = it * 16 + (lane >> 2);
+        const i32x4 v = *(const i32x4*)(wl + q * 64 + (c << 4));
+        const int lc = c ^ ((q >> 2) & 3);
+        if (row0 + q < m_end && ch < a.I)
+          *(i32x4*)(a.out_q + (size_t)(row0 + q) * a.I + ch + 16 * lc) = v;
       }
     } else {
 #pragma unroll
@@ -163,7 +228,7 @@ fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
           for (int tj = 0; tj < v4::TJ; ++tj)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[ti][tj][4 * g + j] *= qsv[tj] * sr[j];
+            for (int j = 0; j < 4; ++j) acc[ti][tj][4 * g + j] *= sr[j];
         }
       char* wl = smem + w * (v4::WQ * v2::EPI_ROWB);
       v2::stage_acc<bf16, v4::TJ>(acc, wl);
@@ -177,7 +242,7 @@ fp8_gemm_kernel(Fp8Args a) {
     if (jn >= t_cnt) break;
     setup(nxt);
     v4::bare_barrier();  // every wave is done with its staging block
-    v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
+    if (PRE) v4::ring_prologue<fp8e4m3>(lp, lq, 0, a.K, smem, 0, 0, v4::NSLOT);
     cur = nxt;
     jt = jn;
   }
@@ -247,40 +312,50 @@ using namespace moe;
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Scale table of the intermediate: one row per K step of the down GEMM (I / 128), 256 bytes per
+// possible token tile (the grouped tiling gives at most ceil(n_rows / 256) + E of them).
+static int64_t bscale_pitch(int64_t n_rows, int E) {
+  return (int64_t)v4::TILE * ((n_rows + v4::TILE - 1) / v4::TILE + E);
+}
+
+extern "C" int64_t moe_fp8_inter_bscale_bytes(int64_t I, int64_t n_rows, int E) {
+  if (I <= 0 || n_rows < 0 || E <= 0) return 0;
+  return (I / 128) * bscale_pitch(n_rows, E);
+}
+
 extern "C" int moe_fp8_fwd(const void* x_q, const float* x_scale, int64_t n_tokens, int64_t H,
                            const void* w13_q, const float* w13_scale, const void* w2_q,
                            const float* w2_scale, int E, int64_t I, const int32_t* offsets,
-                           const int32_t* sorted_token, int64_t n_rows, void* inter,
-                           void* inter_q, float* inter_scale, void* eo, void* stream) {
+                           const int32_t* sorted_token, int64_t n_rows, void* inter_q,
+                           void* inter_bscale, void* eo, void* stream) {
   if (n_tokens < 0 || H <= 0 || I <= 0 || E <= 0 || E > MAX_GLU_EXPERTS || n_rows < 0)
     return MOE_ERR_SHAPE;
   if (H >= (1 << 30) || I >= (1 << 29) || n_rows >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
   if (H % 128 != 0 || I % 128 != 0) return MOE_ERR_ALIGN;
   if (n_rows == 0) return MOE_OK;
   if (!x_q || !x_scale || !w13_q || !w13_scale || !w2_q || !w2_scale || !offsets ||
-      !sorted_token || !inter || !inter_q || !inter_scale || !eo)
+      !sorted_token || !inter_q || !inter_bscale || !eo)
     return MOE_ERR_SHAPE;
   if (!al16(x_q) || !al16(w13_q) || !al16(w2_q) || !al16(w13_scale) || !al16(w2_scale) ||
-      !al16(inter) || !al16(inter_q) || !al16(eo))
+      !al16(inter_q) || !al16(eo))
     return MOE_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
+  const int64_t bs_ld = bscale_pitch(n_rows, E);
   Fp8Args g = {};
   g.P = (const fp8e4m3*)w13_q; g.p_e = 2 * I * H; g.p_ld = H;
   g.p_scale = w13_scale; g.ps_e = 2 * I;
   g.R = (int)(2 * I); g.K = (int)H; g.I = (int)I;
   g.Q = (const fp8e4m3*)x_q; g.q_ld = H; g.q_gather = sorted_token; g.q_scale = x_scale;
   g.offsets = offsets; g.E_glu = E;
-  g.out = (bf16*)inter; g.out_ld = I;
+  g.out_q = (fp8e4m3*)inter_q; g.out_bscale = (uint8_t*)inter_bscale; g.bs_ld = bs_ld;
   int st = launch_fp8<true>(g, n_rows, s);
   if (st) return st;
-  hipLaunchKernelGGL(rowquant_fp8_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, s,
-                     (const bf16*)inter, n_rows, (int)I, (fp8e4m3*)inter_q, inter_scale);
-  if (hipGetLastError() != hipSuccess) return MOE_ERR_LAUNCH;
   Fp8Args d = {};
   d.P = (const fp8e4m3*)w2_q; d.p_e = H * I; d.p_ld = I;
   d.p_scale = w2_scale; d.ps_e = H;
   d.R = (int)H; d.K = (int)I; d.I = (int)I;
-  d.Q = (const fp8e4m3*)inter_q; d.q_ld = I; d.q_gather = nullptr; d.q_scale = inter_scale;
+  d.Q = (const fp8e4m3*)inter_q; d.q_ld = I; d.q_gather = nullptr;
+  d.q_bscale = (const uint8_t*)inter_bscale; d.bs_ld = bs_ld;
   d.offsets = offsets; d.E_glu = E;
   d.out = (bf16*)eo; d.out_ld = H;
   return launch_fp8<false>(d, n_rows, s);

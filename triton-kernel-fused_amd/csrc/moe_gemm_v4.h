@@ -102,6 +102,52 @@ struct KcLoadT {
 using KcLoad = KcLoadT<32>;
 using KcLoad16 = KcLoadT<16>;
 
+// K-contiguous fp8 operand with one E8M0 scale per (row, K step of 128) for the B side of
+// v_mfma_scale_f32_32x32x64_f8f6f4. The scales of K step s sit in byte row s of a table (row
+// pitch s_ld) with 256 bytes per token tile (tile index mt at byte 256 mt), two per lane: bytes
+// 2j and 2j+1 of a wave's 64 are its rows j and j+32, so one 16-bit load gives lane l the scales
+// of its two fragment rows (selected by the MFMA's op_sel, 0 for tj = 0, 1 for tj = 1). The loads
+// are inline asm, like the DMAs, so the compiler adds no waits of its own, and the ring's waits
+// cover them: steps 0 and 1 go out before the prologue's DMAs; step s+2's right after its Q
+// refill in step s's last slab, ahead of the P refill that the next per-step wait leaves in
+// flight. Three registers hold the scales of steps s-1 / s / s+1 (x0 / x1 / x2); shift_scale
+// moves them down and loads step s+2's into x2. fence_scales (after each wait) re-defines x1 and
+// x2 there, so no compiler copy of them can come before it. The prologue must run inside
+// mainloop_ring (PRE = false): its loads are then in flight in straight-line code only.
+struct KcLoadS : KcLoadT<32> {
+  static constexpr bool SCALED = true;
+  const char* sp;  // this lane's scale pair in the table's row 0
+  long long s_ld;
+  unsigned x0 = 0, x1 = 0, x2 = 0;
+  __device__ __forceinline__ const char* at(int k) const { return sp + (long long)(k >> 7) * s_ld; }
+  // The scales of K steps k0 and k1, loaded ahead of the prologue's DMAs. The loads (and the
+  // shift below) write the registers in place through tied asm operands, so the three values keep
+  // their registers across the loop and no compiler copy reads a register whose load is still in
+  // flight.
+  __device__ __forceinline__ void prologue_scales(int k0, int k1) {
+    asm volatile("global_load_ushort %0, %2, off\n\tglobal_load_ushort %1, %3, off"
+                 : "+v"(x1), "+v"(x2)
+                 : "v"(at(k0)), "v"(at(k1))
+                 : "memory");
+  }
+  __device__ __forceinline__ void shift_scale(int k) {
+    asm volatile("v_mov_b32 %0, %1\n\tv_mov_b32 %1, %2\n\tglobal_load_ushort %2, %3, off"
+                 : "+v"(x0), "+v"(x1), "+v"(x2)
+                 : "v"(at(k))
+                 : "memory");
+  }
+  __device__ __forceinline__ void fence_scales() { asm volatile("" : "+v"(x1), "+v"(x2)); }
+};
+// Loaders with per-step B scales (KcLoadS) declare SCALED = true.
+template <class L, class = void>
+struct Scaled : std::false_type {};
+template <class L>
+struct Scaled<L, std::void_t<decltype(L::SCALED)>> : std::bool_constant<L::SCALED> {};
+template <class L>
+__device__ __forceinline__ void shift_scale_of(L& l, int k) {
+  if constexpr (Scaled<L>::value) l.shift_scale(k);
+}
+
 // Row-contiguous operand (element (r, k) at src + row(k) * ld + 2r, src at column r0; row(k) =
 // gather[k] or k): [64 K rows][256 r x 2 bytes], the 16-byte chunk index XOR-ed by 4 * (k & 3)
 // (the XOR applies to the whole chunk index: wave blocks of 64 columns start at odd multiples of 8).
@@ -257,6 +303,7 @@ __device__ __forceinline__ void ring_prologue(LP& lp, LQ& lq, int k0, int k1, ch
   if (first == 0) {
     lp.prime(k0);
     lq.prime(k0);
+    if constexpr (Scaled<LQ>::value) lq.prologue_scales(k0, min(k0 + KS, klast));
   }
   for (int i = first; i < first + count; ++i) {
     const int si = base + i >= NSLOT ? base + i - NSLOT : base + i;
@@ -295,10 +342,12 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
   constexpr int PRO = ROLL ? NSLOT : NSLOT - 1;  // FB == 2: P2 goes out with step 0's slab 0
   static_assert(!PRE || ROLL, "a pre-issued prologue is implemented for the ROLL schedule");
   if constexpr (!PRE) ring_prologue<T>(lp, lq, k0, k1, smem, base, 0, PRO);
+  static_assert(!Scaled<LQ>::value || (ROLL && !PRE), "block scales need the ROLL schedule and an in-loop prologue");
   wait_slots(PRO - 2);
   // Pending P refill (slot, K) issued during the next step's first slab.
   int pp_slot = base == 0 ? NSLOT - 1 : base - 1, pp_k = min(k0 + 2 * KS, klast);
   bare_barrier();
+  if constexpr (Scaled<LQ>::value) lq.fence_scales();
 
   constexpr int FB = ROLL ? 1 : 2;
   i32x4 a[FB][TI_][CPL], b[FB][TJ_][CPL];
@@ -351,6 +400,7 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
         if (sync) {
           wait_slots(1);
           bare_barrier();
+          if constexpr (Scaled<LQ>::value) lq.fence_scales();
           kq = min(k0 + (s + 2) * KS, klast);
           kp = min(k0 + (s + 3) * KS, klast);
         }
@@ -359,7 +409,15 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
         __builtin_amdgcn_sched_barrier(0);
         static_for<0, NM>([&](auto ic) {
           constexpr int I = decltype(ic)::value;
-          if constexpr (COMPUTE) Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
+          if constexpr (COMPUTE) {
+            if constexpr (Scaled<LQ>::value) {
+              // MFMAs after this slab's shift_scale find step s's scales in x0.
+              const unsigned sc = (sync && I >= LOADS * DI) ? lq.x0 : lq.x1;
+              Mfma<T>::template stepf_sb<I % TJ_>(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_], sc);
+            } else {
+              Mfma<T>::stepf(acc[I / TJ_][I % TJ_], ra[I / TJ_], rb[f][I % TJ_]);
+            }
+          }
           __builtin_amdgcn_sched_barrier(0);
           if constexpr (COMPUTE && I < TJ_) {
 #pragma unroll
@@ -376,6 +434,7 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
             if (sync) {
               if constexpr (d < LOADS) lq.template issue_i<T, d>(qslot, kq);
               else lp.template issue_i<T, d - LOADS>(pslot, kp);
+              if constexpr (d == LOADS - 1) shift_scale_of(lq, kq);
             }
           }
           __builtin_amdgcn_sched_barrier(0);

@@ -44,7 +44,8 @@ _SIGS = {
     "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_glu_fwd": [_I, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P],
     "moe_glu_bwd": [_I, _P, _L, _L, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P],
-    "moe_fp8_fwd": [_P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P, _P, _P],
+    "moe_fp8_fwd": [_P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P, _P],
+    "moe_fp8_inter_bscale_bytes": [_L, _L, _I],
     "moe_rowquant_fp8": [_P, _L, _L, _P, _P, _P],
     "moe_router_topk_fwd": [_I, _P, _L, _L, _I, _P, _I, _I, _I, _F, _P, _P, _P, _P],
     "moe_router_topk_bwd": [_I, _P, _L, _L, _I, _P, _P, _I, _I, _I, _F, _P, _L, _P],
@@ -52,7 +53,8 @@ _SIGS = {
     "moe_mxfp8_fwd": [_P, _L, _L, _P, _P, _P, _P, _I, _L, _P, _P, _L, _P, _P, _P],
 }
 _RESTYPES = {"moe_version": ctypes.c_char_p, "moe_gate_grad_parts": ctypes.c_int, "moe_get_workspace_size": ctypes.c_size_t,
-             "moe_token_split_workspace_size": ctypes.c_size_t}
+             "moe_token_split_workspace_size": ctypes.c_size_t,
+             "moe_fp8_inter_bscale_bytes": ctypes.c_int64}
 
 _ERRORS = {
     1: (ValueError, "shape"),

@@ -10,8 +10,9 @@ dispatch and gate-weighted combine. Formats (produce them with kernels.gfx950.qu
          gate_up_scale (E,2I) fp32 per output channel; down_q (E,H,I) + down_scale (E,H).
   MXFP8: hidden (N,H) bf16; gate_up_q (E,2I,H) e4m3 + gate_up_scale (E,2I,H/32) uint8 E8M0;
          down_q (E,H,I) + down_scale (E,H,I/32).
-The fp8 path re-quantises the SwiGLU intermediate per routed row (absmax/448) before the down
-projection. Output: (N,H) bf16.
+The fp8 path re-quantises the SwiGLU intermediate before the down projection with one
+power-of-two scale per routed row and 128-channel block (the smallest 2^e with 448 * 2^e >= the
+block's absmax; oracle.moe_oracle.e8m0_block_requant states it). Output: (N,H) bf16.
 """
 import torch
 
@@ -59,17 +60,17 @@ def moe_fp8(x_q, x_scale, top_k_indices, top_k_weights, gate_up_q, gate_up_scale
     wt = top_k_weights.to(torch.bfloat16).contiguous()
     m = idx.numel()
     routing = _Routing(idx, e)
-    inter = torch.empty(m, inter_dim, device=dev, dtype=torch.bfloat16)
     inter_q = torch.empty(m, inter_dim, device=dev, dtype=torch.float8_e4m3fn)
-    inter_s = torch.empty(max(m, 1), device=dev, dtype=torch.float32)
+    inter_bs = torch.empty(max(1, _lib.lib().moe_fp8_inter_bscale_bytes(inter_dim, m, e)),
+                           device=dev, dtype=torch.uint8)
     eo = torch.empty(m, h, device=dev, dtype=torch.bfloat16)
     if m:
         _lib.call("moe_fp8_fwd", _lib.ptr(x_q.contiguous()), _lib.ptr(x_scale.float().contiguous()),
                   n_tok, h, _lib.ptr(gate_up_q.contiguous()),
                   _lib.ptr(gate_up_scale.float().contiguous()), _lib.ptr(down_q.contiguous()),
                   _lib.ptr(down_scale.float().contiguous()), e, inter_dim,
-                  _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token), m, _lib.ptr(inter),
-                  _lib.ptr(inter_q), _lib.ptr(inter_s), _lib.ptr(eo), _lib.stream_of(dev))
+                  _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token), m, _lib.ptr(inter_q),
+                  _lib.ptr(inter_bs), _lib.ptr(eo), _lib.stream_of(dev))
     return _combine(eo, wt, idx, routing, n_tok, h, e)
 
 
