@@ -83,12 +83,16 @@ __device__ __forceinline__ int slot_kind(int64_t e, const int32_t* codes, int E_
   return c == 3 ? 1 : 2;
 }
 
-// Per-token gathers (combine forward, un-permute backward). One wave owns one 64*V-column chunk
-// of one token; the k routed rows are loaded BATCH at a time, all BATCH loads in flight together
-// (the token's routing reads are wave-uniform), and summed in slot order in fp32:
+// Per-token gathers (combine forward, un-permute backward). One wave owns CPW 64*V-column chunks
+// of one token; the k routed rows are loaded BATCH at a time, all BATCH x CPW loads in flight
+// together (the token's routing reads are wave-uniform), and summed in slot order in fp32:
 //   acc = sum_j g_j * row_j,  row_j = rows[f2s[t,j]] for a GLU expert (g_j = gate if GATE_GLU,
 //   else 1) or self[t] for an Identity expert (g_j = gate); Zero experts and invalid ids add
 //   nothing.
+// Column chunks per wave in the per-token gathers: two put 16 loads in flight behind one round of
+// routing reads (measured ~4% faster than one; four is level).
+constexpr int CPW = 2;
+
 template <typename T, bool GATE_GLU, int BATCH>
 __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T* __restrict__ self,
                                              int64_t self_ld, const T* __restrict__ wt,
@@ -98,47 +102,58 @@ __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T
                                              int64_t N, int k, int H, T* __restrict__ out) {
   constexpr int V = Vec8<T>::N;
   const int nchunk = (H + 64 * V - 1) / (64 * V);
+  const int ncw = (nchunk + CPW - 1) / CPW;
   const int64_t wv = (int64_t)blockIdx.x * (ROW_THREADS / 64) + (threadIdx.x >> 6);
-  if (wv >= N * nchunk) return;
-  const int64_t t = wv / nchunk;
+  if (wv >= N * ncw) return;
+  const int64_t t = wv / ncw;
   const int lane = threadIdx.x & 63;
-  {
-    const int c = (int)(wv % nchunk) * 64 * V + lane * V;
-    const bool col_ok = c < H;
-    float acc[V];
+  int c[CPW];
+  bool col_ok[CPW];
+  float acc[CPW][V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int j0 = 0; j0 < k; j0 += BATCH) {
-      // Branch-free: every slot's 16 bytes are loaded (a skipped slot reads the token's own row)
-      // before any is used, so the BATCH loads are in flight together.
-      const T* src[BATCH];
-      float w[BATCH];
-      bool used[BATCH];
+  for (int u = 0; u < CPW; ++u) {
+    c[u] = ((int)(wv % ncw) * CPW + u) * 64 * V + lane * V;
+    col_ok[u] = c[u] < H;
 #pragma unroll
-      for (int jj = 0; jj < BATCH; ++jj) {
-        const int j = j0 + jj;
-        const int64_t f = t * k + (j < k ? j : 0);
-        const int pos = f2s[f];
-        const int kind = j < k ? slot_kind(idx[f], codes, E_glu, E_all, pos) : 2;
-        used[jj] = kind != 2 && col_ok;
-        w[jj] = (kind == 0 && !GATE_GLU) ? 1.f : to_f32(wt[f]);
-        src[jj] = kind == 0 ? rows + (size_t)pos * H : self + (size_t)t * self_ld;
-      }
-      i32x4 raw[BATCH];
-      const int cc = col_ok ? c : 0;
+    for (int i = 0; i < V; ++i) acc[u][i] = 0.f;
+  }
+  for (int j0 = 0; j0 < k; j0 += BATCH) {
+    // Branch-free: every slot's 16 bytes are loaded (a skipped slot reads the token's own row)
+    // before any is used, so the BATCH x CPW loads are in flight together.
+    const T* src[BATCH];
+    float w[BATCH];
+    bool used[BATCH];
 #pragma unroll
-      for (int jj = 0; jj < BATCH; ++jj) raw[jj] = *(const i32x4*)(src[jj] + cc);
+    for (int jj = 0; jj < BATCH; ++jj) {
+      const int j = j0 + jj;
+      const int64_t f = t * k + (j < k ? j : 0);
+      const int pos = f2s[f];
+      const int kind = j < k ? slot_kind(idx[f], codes, E_glu, E_all, pos) : 2;
+      used[jj] = kind != 2;
+      w[jj] = (kind == 0 && !GATE_GLU) ? 1.f : to_f32(wt[f]);
+      src[jj] = kind == 0 ? rows + (size_t)pos * H : self + (size_t)t * self_ld;
+    }
+    i32x4 raw[CPW][BATCH];
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int cc = col_ok[u] ? c[u] : 0;
+#pragma unroll
+      for (int jj = 0; jj < BATCH; ++jj) raw[u][jj] = *(const i32x4*)(src[jj] + cc);
+    }
+#pragma unroll
+    for (int u = 0; u < CPW; ++u)
 #pragma unroll
       for (int jj = 0; jj < BATCH; ++jj) {
         float v[V];
-        Vec8<T>::ld((const T*)&raw[jj], v);
+        Vec8<T>::ld((const T*)&raw[u][jj], v);
         // A skipped slot contributes nothing (not even 0 * inf).
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] += used[jj] ? w[jj] * v[i] : 0.f;
+        for (int i = 0; i < V; ++i) acc[u][i] += used[jj] ? w[jj] * v[i] : 0.f;
       }
-    }
-    if (col_ok) Vec8<T>::st(out + (size_t)t * H + c, acc);
   }
+#pragma unroll
+  for (int u = 0; u < CPW; ++u)
+    if (col_ok[u]) Vec8<T>::st(out + (size_t)t * H + c[u], acc[u]);
 }
 
 // out[t] = sum_j w[t,j] * row(t,j); GATE_GLU false: GLU rows already carry their gate.
@@ -435,7 +450,9 @@ static unsigned row_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
 // Waves per token for the per-token gathers (combine, un-permute): one per 64*vec-column chunk.
 // Each wave keeps its token's 8 row loads in flight together; whole-token waves loading one row
 // at a time measured ~20% slower even when the grid alone fills the GPU.
-static int64_t token_col_waves(int64_t H, int vec) { return (H + 64 * vec - 1) / (64 * vec); }
+static int64_t token_col_waves(int64_t H, int vec) {
+  return ((H + 64 * vec - 1) / (64 * vec) + CPW - 1) / CPW;
+}
 
 extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
                                const void* top_k_weights, const int64_t* top_k_indices,
