@@ -56,31 +56,34 @@ constexpr int MX_BATCH = 8;       // staging loads in flight per lane
 
 // Scale-table row stride in 4-byte words for nc K chunks split over the waves: one word (four
 // E8M0 bytes) per chunk, rounded up to an odd count so the 16 rows of a tile hit distinct banks.
-__host__ __device__ inline int mx_scale_words(int nc) {
-  return ((nc + MX_WAVES - 1) / MX_WAVES) | 1;
+__host__ __device__ inline int mx_scale_words(int nc, bool ks) {
+  return (ks ? (nc + MX_WAVES - 1) / MX_WAVES : nc) | 1;
 }
 
 // One block per (expert, RT consecutive row tiles of 64 weight rows): gate/up tile = rows
 // ch..ch+31 of the gate and the same channels of up (GLU), down tile = 64 rows. The block stages
-// the expert's token rows once and runs its row tiles one after the other over them. Wave w
-// streams K chunks [w*nc/4, (w+1)*nc/4) of all 64 rows of a tile; the partial sums meet in LDS.
+// the expert's token rows once and runs its row tiles over them. KS (K split, long K): wave w
+// streams K chunks [w*nc/4, (w+1)*nc/4) of every tile of the block, one tile after the other, and
+// the partial sums meet in LDS. Otherwise (short K) wave w streams the whole K of tiles w, w+4,
+// ... on its own and stores them: no exchange and no barrier between tiles.
 //
 // MFMA layout (16x16x32): lane l holds row l%16 of a 16-row weight tile and token l%16 of the
 // token tile; q = l/16 selects K. Within a 128-byte chunk lane q owns the weight bytes
 // [32q, 32q+32) (after the load exchange below), consumed as four K steps of 8; the token
 // fragments use the same K order. Those 32 bytes are exactly scale block q of the chunk.
 //
-// LDS: RT x 4 per-wave scale tables ([64 rows][sw words] each), then (RT > 1) the partial-sum
-// exchange, then the staged token rows (RT == 1: the exchange reuses the token rows' space).
+// LDS: the scale tables ([64 rows][sw words] each; KS: RT x 4 per wave and tile, else RT, one per
+// tile), then (KS, RT > 1) the partial-sum exchange, then the staged token rows (KS, RT == 1: the
+// exchange reuses the token rows' space).
 constexpr int MX_RED_BYTES = MX_WAVES * 4 * 64 * 16;  // [wave][tile][lane] f32x4
-__host__ __device__ inline int mx_table_bytes(int nc, int rt) {
-  return rt * MX_WAVES * MX_ROWS * mx_scale_words(nc) * 4;
+__host__ __device__ inline int mx_table_bytes(int nc, int rt, bool ks) {
+  return rt * (ks ? MX_WAVES : 1) * MX_ROWS * mx_scale_words(nc, ks) * 4;
 }
-__host__ __device__ inline int mx_x_offset(int nc, int rt) {
-  return mx_table_bytes(nc, rt) + (rt > 1 ? MX_RED_BYTES : 0);
+__host__ __device__ inline int mx_x_offset(int nc, int rt, bool ks) {
+  return mx_table_bytes(nc, rt, ks) + (ks && rt > 1 ? MX_RED_BYTES : 0);
 }
 
-template <bool GLU, int RT>
+template <bool GLU, int RT, bool KS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 mx_gemm_kernel(MxArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -96,14 +99,20 @@ mx_gemm_kernel(MxArgs a) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rr = lane & 15, q = lane >> 4;
   const int nc = a.K / 128;
-  const int c0 = w * nc / MX_WAVES, nch = (w + 1) * nc / MX_WAVES - c0;  // >= 1: K % 512 == 0
+  // >= 1 chunk per wave: K % 512 == 0
+  const int c0 = KS ? w * nc / MX_WAVES : 0, nch = KS ? (w + 1) * nc / MX_WAVES - c0 : nc;
   auto chunk = [&](int i) { return c0 + i; };  // the wave's i-th K chunk
-  const int total = nrt * nch;      // (tile, chunk) items of this wave, tile-major
-  const int sw = mx_scale_words(nc);
-  auto stab_of = [&](int j) { return (uint32_t*)lds + (j * MX_WAVES + w) * MX_ROWS * sw; };
-  char* xlds = lds + mx_x_offset(nc, RT);
-  f32x4* red = (f32x4*)(RT > 1 ? lds + mx_table_bytes(nc, RT) : xlds);
-  const int x_bytes = MX_LDS - mx_x_offset(nc, RT);
+  // The wave's tiles: tile(j), j < nrt_w.
+  const int nrt_w = KS ? nrt : (w < nrt ? (nrt - w + MX_WAVES - 1) / MX_WAVES : 0);
+  auto tile = [&](int j) { return rt0 + (KS ? j : w + MX_WAVES * j); };
+  const int total = nrt_w * nch;    // (tile, chunk) items of this wave, tile-major
+  const int sw = mx_scale_words(nc, KS);
+  auto stab_of = [&](int j) {
+    return (uint32_t*)lds + (KS ? j * MX_WAVES + w : w + MX_WAVES * j) * MX_ROWS * sw;
+  };
+  char* xlds = lds + mx_x_offset(nc, RT, KS);
+  f32x4* red = (f32x4*)(RT > 1 ? lds + mx_table_bytes(nc, RT, KS) : xlds);
+  const int x_bytes = MX_LDS - mx_x_offset(nc, RT, KS);
   // Block barrier without HIP's release fence: weight loads stay in flight across it.
   auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
@@ -130,7 +139,7 @@ mx_gemm_kernel(MxArgs a) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj)
-        roff[t][jj] = (uint32_t)wrow(rt0 + j, 16 * t + 8 * jj + r8) * (uint32_t)a.w_ld + 16 * pc;
+        roff[t][jj] = (uint32_t)wrow(tile(j), 16 * t + 8 * jj + r8) * (uint32_t)a.w_ld + 16 * pc;
   };
   set_rows(0);
 
@@ -150,7 +159,7 @@ mx_gemm_kernel(MxArgs a) {
             (const i32x4*)(wexp + (size_t)chunk(fc) * 128 + roff[t][jj]));
     __builtin_amdgcn_sched_barrier(0);
     if (++fc == nch) {
-      if (fj + 1 < nrt) {
+      if (fj + 1 < nrt_w) {
         ++fj;
         fc = 0;
         set_rows(fj);
@@ -164,7 +173,7 @@ mx_gemm_kernel(MxArgs a) {
   // loads go out in batches of MX_BATCH per lane before any of them is written to LDS, so a
   // block start waits for a few load latencies rather than one per element.
   fetch(p0);
-  for (int j = 0; j < nrt; ++j) {
+  for (int j = 0; j < nrt_w; ++j) {
     uint32_t* stab = stab_of(j);
     const int n = MX_ROWS * nch;
     for (int u0 = lane; u0 < n; u0 += 64 * MX_BATCH) {
@@ -173,7 +182,7 @@ mx_gemm_kernel(MxArgs a) {
       for (int b = 0; b < MX_BATCH; ++b) {
         const int u = min(u0 + 64 * b, n - 1);  // past the end: re-read the last word
         const int i = u / nch, c = u % nch;
-        v[b] = *(const uint32_t*)(a.S + (size_t)e * a.s_e + (size_t)wrow(rt0 + j, i) * a.s_ld +
+        v[b] = *(const uint32_t*)(a.S + (size_t)e * a.s_e + (size_t)wrow(tile(j), i) * a.s_ld +
                                   chunk(c) * 4);
       }
 #pragma unroll
@@ -264,25 +273,29 @@ mx_gemm_kernel(MxArgs a) {
           }
         }
       };
-      // After the last chunk of tile cj: partial sums of waves 1-3 meet wave 0's in LDS, wave 0
-      // stores the tile.
+      // After the last chunk of tile cj. KS: partial sums of waves 1-3 meet wave 0's in LDS,
+      // wave 0 stores the tile. Otherwise the wave stores its own tile.
       auto finish_tile = [&]() {
-        if (RT == 1) barrier();  // the exchange reuses the token rows' space
-        if (w > 0) {
+        if (KS) {
+          if (RT == 1) barrier();  // the exchange reuses the token rows' space
+          if (w > 0) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
+            for (int t = 0; t < 4; ++t) red[(w * 4 + t) * 64 + lane] = acc[t];
+          }
+          barrier();
         }
-        barrier();
-        if (w == 0) {
+        if (!KS || w == 0) {
+          if (KS) {
 #pragma unroll
-          for (int v = 1; v < MX_WAVES; ++v)
+            for (int v = 1; v < MX_WAVES; ++v)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const f32x4 p = red[(v * 4 + t) * 64 + lane];
+              for (int t = 0; t < 4; ++t) {
+                const f32x4 p = red[(v * 4 + t) * 64 + lane];
 #pragma unroll
-              for (int jj = 0; jj < 4; ++jj) acc[t][jj] += p[jj];
-            }
-          const int rt = rt0 + cj;
+                for (int jj = 0; jj < 4; ++jj) acc[t][jj] += p[jj];
+              }
+          }
+          const int rt = tile(cj);
           // Lane (token rr, q) holds rows 4q .. 4q+3 of each 16-row tile.
           if (rr < nt) {
             bf16* o = a.out + (size_t)m * a.out_ld;
@@ -306,7 +319,7 @@ mx_gemm_kernel(MxArgs a) {
             }
           }
         }
-        if (RT > 1) barrier();  // wave 0 has read the exchange before the next tile writes it
+        if (KS && RT > 1) barrier();  // wave 0 has read the exchange before the next tile writes it
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
       };
@@ -343,14 +356,20 @@ using namespace moe;
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // Row tiles per block: several when the scale tables of that many tiles, the partial-sum
-// exchange and at least 16 KB of token rows fit the block's LDS. The down projection's blocks are
-// short (K = I), so four tiles per block amortise the staging (measured 4% faster than two on
-// config 5); the gate/up projection measured level from one to two.
+// exchange and at least 16 KB of token rows fit the block's LDS. The gate/up projection (long K)
+// splits K over the waves, two tiles per block (level with one); the down projection (short K,
+// K = I) gives each wave a tile of its own, four per block.
 #ifndef MX_RT_GLU
 #define MX_RT_GLU 2
 #endif
 #ifndef MX_RT_DOWN
 #define MX_RT_DOWN 4
+#endif
+#ifndef MX_KS_DOWN
+#define MX_KS_DOWN false
+#endif
+#ifndef MX_KS_GLU
+#define MX_KS_GLU true
 #endif
 template <bool GLU>
 static bool launch_mx(const MxArgs& a, int E, hipStream_t s) {
@@ -361,8 +380,9 @@ static bool launch_mx(const MxArgs& a, int E, hipStream_t s) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, MX_LDS);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * MX_WAVES), MX_LDS, s, a);
   };
-  if (MX_RT > 1 && mx_x_offset(nc, MX_RT) + 16384 <= MX_LDS) go(mx_gemm_kernel<GLU, MX_RT>, MX_RT);
-  else go(mx_gemm_kernel<GLU, 1>, 1);
+  constexpr bool KS = GLU ? MX_KS_GLU : MX_KS_DOWN;
+  if (MX_RT > 1 && mx_x_offset(nc, MX_RT, KS) + 16384 <= MX_LDS) go(mx_gemm_kernel<GLU, MX_RT, KS>, MX_RT);
+  else go(mx_gemm_kernel<GLU, 1, KS>, 1);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -381,9 +401,9 @@ extern "C" int moe_mxfp8_fwd(const void* hidden, int64_t n_tokens, int64_t H, co
       ((uintptr_t)w13_scale & 3) || ((uintptr_t)w2_scale & 3))
     return MOE_ERR_ALIGN;
   // The scale tables of a block plus the partial sums (16 KB) must fit the block's LDS.
-  for (int64_t k : {H, I})
-    if (mx_x_offset((int)(k / 128), 1) + MX_RED_BYTES > MX_LDS)
-      return MOE_ERR_SHAPE;
+  if (mx_x_offset((int)(H / 128), 1, MX_KS_GLU) + MX_RED_BYTES > MX_LDS ||
+      mx_x_offset((int)(I / 128), 1, MX_KS_DOWN) + MX_RED_BYTES > MX_LDS)
+    return MOE_ERR_SHAPE;
   if ((int64_t)E * ((2 * I + 63) / 64) >= ((int64_t)1 << 31)) return MOE_ERR_SHAPE;
   // Row offsets within one expert's weights are 32-bit.
   if (2 * I * H >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
