@@ -17,7 +17,7 @@ block's absmax; oracle.moe_oracle.e8m0_block_requant states it). Output: (N,H) b
 import torch
 
 from .. import _lib
-from .moe import _Routing
+from .moe import _CHECK_INDICES, _Routing
 
 __all__ = ["moe_fp8", "moe_mxfp8", "rowquant_fp8"]
 
@@ -37,9 +37,15 @@ def _check_common(idx, wt, n_tokens, gate_up_q, down_q):
     return e, h, two_i // 2
 
 
+_ZERO_CODES = {}   # (device index, E) -> all-SwiGLU act codes, read-only
+
+
 def _combine(eo, wt, idx, routing, n_tok, h, e):
     out = torch.empty(n_tok, h, device=eo.device, dtype=torch.bfloat16)
-    codes = torch.zeros(e, device=eo.device, dtype=torch.int32)
+    key = (eo.device.index, e)
+    codes = _ZERO_CODES.get(key)
+    if codes is None:
+        codes = _ZERO_CODES[key] = torch.zeros(e, device=eo.device, dtype=torch.int32)
     _lib.call("moe_combine_fwd", _lib.dtype_code(torch.bfloat16), _lib.ptr(eo), _lib.ptr(eo),
               _lib.ptr(wt), _lib.ptr(idx), _lib.ptr(codes), e, e, _lib.ptr(routing.flat_to_sorted),
               n_tok, idx.shape[1], h, 0, _lib.ptr(out), _lib.stream_of(eo.device))
@@ -59,7 +65,7 @@ def moe_fp8(x_q, x_scale, top_k_indices, top_k_weights, gate_up_q, gate_up_scale
     idx = top_k_indices.contiguous()
     wt = top_k_weights.to(torch.bfloat16).contiguous()
     m = idx.numel()
-    routing = _Routing(idx, e)
+    routing = _Routing(idx, e, want_status=_CHECK_INDICES)
     inter_q = torch.empty(m, inter_dim, device=dev, dtype=torch.float8_e4m3fn)
     inter_bs = torch.empty(max(1, _lib.lib().moe_fp8_inter_bscale_bytes(inter_dim, m, e)),
                            device=dev, dtype=torch.uint8)
@@ -89,7 +95,7 @@ def moe_mxfp8(hidden, top_k_indices, top_k_weights, gate_up_q, gate_up_scale, do
     idx = top_k_indices.contiguous()
     wt = top_k_weights.to(torch.bfloat16).contiguous()
     m = idx.numel()
-    routing = _Routing(idx, e)
+    routing = _Routing(idx, e, want_status=_CHECK_INDICES)
     inter = torch.empty(m, inter_dim, device=dev, dtype=torch.bfloat16)
     eo = torch.empty(m, h, device=dev, dtype=torch.bfloat16)
     if m:

@@ -93,10 +93,23 @@ def _check_inputs(hidden, idx, wt, gate_up_proj, down_proj, act_codes):
         raise TypeError("top_k_indices must be int64")
 
 
-class _Routing:
-    """Device-resident dispatch result (see moe_dispatch in include/moe_gfx950.h)."""
+_STATUS_SINK = {}   # device index -> int32 scratch for dispatch counts nobody reads
 
-    def __init__(self, idx, n_experts):
+
+def _status_sink(dev):
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    t = _STATUS_SINK.get(key)
+    if t is None:
+        t = _STATUS_SINK[key] = torch.zeros(1, device=dev, dtype=torch.int32)
+    return t
+
+
+class _Routing:
+    """Device-resident dispatch result (see moe_dispatch in include/moe_gfx950.h). With
+    want_status False the out-of-range count goes to a per-device scratch word that is never read
+    (no zero-fill launch per call); `status` is then None."""
+
+    def __init__(self, idx, n_experts, want_status=True):
         dev = idx.device
         n, k = idx.shape
         m = n * k
@@ -109,15 +122,16 @@ class _Routing:
         self.sorted_token = torch.empty(max(m, 1), **i32)
         self.sorted_flat = torch.empty(max(m, 1), **i32)
         self.flat_to_sorted = torch.empty(max(m, 1), **i32)
-        self.status = torch.zeros(1, **i32)
+        status = torch.zeros(1, **i32) if want_status else _status_sink(dev)
+        self.status = status if want_status else None
         ws = _lib.lib().moe_get_workspace_size(n, k, n_experts)
         self.workspace = torch.empty(max(ws, 256), device=dev, dtype=torch.uint8)
         _lib.call("moe_dispatch", _lib.ptr(idx), n, k, n_experts, _lib.ptr(self.counts),
                   _lib.ptr(self.offsets), _lib.ptr(self.tile_offsets), _lib.ptr(self.expert_order),
                   _lib.ptr(self.sorted_token),
-                  _lib.ptr(self.sorted_flat), _lib.ptr(self.flat_to_sorted), _lib.ptr(self.status),
+                  _lib.ptr(self.sorted_flat), _lib.ptr(self.flat_to_sorted), _lib.ptr(status),
                   _lib.ptr(self.workspace), self.workspace.numel(), _lib.stream_of(dev))
-        if _CHECK_INDICES and int(self.status.item()) != 0:
+        if want_status and _CHECK_INDICES and int(self.status.item()) != 0:
             raise ValueError(f"{int(self.status.item())} top_k_indices outside [0, {n_experts})")
 
     def row_expert(self, n_experts, m):
@@ -176,7 +190,7 @@ class _MoEFunction(torch.autograd.Function):
         m = n_tok * k
         dev = hidden.device
         stream = _lib.stream_of(dev)
-        routing = _Routing(idx, n_exp)
+        routing = _Routing(idx, n_exp, want_status=_CHECK_INDICES)
 
         gate_up = torch.empty(m, two_i, device=dev, dtype=dt)
         inter = torch.empty(m, inter_dim, device=dev, dtype=dt)
