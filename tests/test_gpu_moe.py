@@ -115,6 +115,19 @@ def test_bf16_parity_vs_oracle(name, codes, e_glu, cap):
     _assert_bf16(mine, ref, (hid, idx, w, gu, dw, go), codes)
 
 
+def test_bf16_max_experts():
+    """MAX_GLU_EXPERTS = 1024 experts, ~5 rows each (many empty), top-8: the dispatch's largest
+    histogram, the GEMMs' expert walk over 1024 groups and the gated backward."""
+    e = 1024
+    hid, idx, w, gu, dw, codes_t, ap, go = _case([0] * e, e, dtype=torch.bfloat16, n=600, h=128,
+                                                 i=128, k=8, seed=3)
+    _say("bf16 1024 experts")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, [0] * e, go, dtype=torch.float64)
+    dev = [t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)]
+    mine = _run(kernels.moe, *dev)
+    _assert_bf16(mine, ref, (hid, idx, w, gu, dw, go), [0] * e)
+
+
 def test_fp16_parity_vs_oracle():
     hid, idx, w, gu, dw, codes_t, ap, go = _case([0, 1, 0, 0], 4, dtype=torch.float16, n=300)
     _say("fp16 silu/relu2")
