@@ -109,6 +109,30 @@ def test_mxfp8_many_tokens_per_expert():
 
 
 @pytest.mark.parametrize("fmt", ["fp8", "mxfp8"])
+def test_quantised_forwards_skip_out_of_range_ids_and_empty_experts(fmt):
+    """Ids outside [0, E) add nothing (as in the bf16 path); experts 0 and E-1 receive no rows;
+    several expert groups span more than one 256-row tile with ragged tails."""
+    cfg = 4 if fmt == "fp8" else 5
+    w = make_workload(cfg, seed=4, scale=dict(N=600, H=512, I=512, E=6, k=2))
+    idx = w["idx"].clone()
+    idx[idx == 0] = 1
+    idx[idx == 5] = 2
+    idx[::7, 0] = -1
+    idx[3::11, 1] = 6
+    _say(f"{fmt} out-of-range ids, empty experts")
+    if fmt == "fp8":
+        args = (w["x_q"], w["x_scale"], idx, w["wt"], w["gate_up_q"], w["gate_up_scale"],
+                w["down_q"], w["down_scale"])
+        ref, fn = orc.fp8_forward(*args), kernels.moe_fp8
+    else:
+        args = (w["hidden"], idx, w["wt"], w["gate_up_q"], w["gate_up_scale"], w["down_q"],
+                w["down_scale"])
+        ref, fn = orc.mxfp8_forward(*args), kernels.moe_mxfp8
+    out = fn(*[t.cuda() for t in args]).cpu()
+    assert _frob(out, ref) <= 3e-3
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp8"])
 def test_forward_from_persisted_weights(tmp_path, fmt):
     """Weights written by quant.save_experts and read back feed the kernels with no re-layout; the
     result is bit-identical to the call with the in-memory quantised weights."""
