@@ -156,3 +156,71 @@ def test_forward_from_persisted_weights(tmp_path, fmt):
                                                   "down_scale")))
     b = fn(*head, *tail, *(t2[k] for k in ("gate_up_q", "gate_up_scale", "down_q", "down_scale")))
     assert torch.equal(a, b)
+
+
+def test_fp8_intermediate_block_scales_follow_the_rule():
+    """The gate/up epilogue's re-quantisation, read back from the library's buffers: every E8M0
+    code is the oracle's rule (smallest 2^e with 448 * 2^e >= the block absmax) applied to the
+    fp64 intermediate, except where that absmax lies within fp32 rounding of a power-of-two
+    boundary, and every dequantised value is within an e4m3 step of the fp64 intermediate (half a
+    step except for under 1% of values, which the kernel's fp32 arithmetic put across a
+    rounding midpoint), up to the fp32 GEMM's error on values that cancel to almost nothing."""
+    from kernels import _lib
+    from kernels.gfx950.moe import _Routing
+    w = make_workload(4, seed=5, scale=dict(N=700, H=256, I=384, E=5, k=2))
+    _say("fp8 intermediate block scales")
+    e, two_i, h = w["gate_up_q"].shape
+    i_dim = two_i // 2
+    idx = w["idx"].cuda().contiguous()
+    m = idx.numel()
+    routing = _Routing(idx, e)
+    iq = torch.empty(m, i_dim, device="cuda", dtype=torch.float8_e4m3fn)
+    nb = _lib.lib().moe_fp8_inter_bscale_bytes(i_dim, m, e)
+    bs = torch.empty(nb, device="cuda", dtype=torch.uint8)
+    eo = torch.empty(m, h, device="cuda", dtype=torch.bfloat16)
+    d = {k: w[k].cuda().contiguous() for k in ("x_q", "x_scale", "gate_up_q", "gate_up_scale",
+                                                "down_q", "down_scale")}
+    _lib.call("moe_fp8_fwd", _lib.ptr(d["x_q"]), _lib.ptr(d["x_scale"].float()), w["x_q"].shape[0],
+              h, _lib.ptr(d["gate_up_q"]), _lib.ptr(d["gate_up_scale"].float()),
+              _lib.ptr(d["down_q"]), _lib.ptr(d["down_scale"].float()), e, i_dim,
+              _lib.ptr(routing.offsets), _lib.ptr(routing.sorted_token), m, _lib.ptr(iq),
+              _lib.ptr(bs), _lib.ptr(eo), _lib.stream_of(idx.device))
+    torch.cuda.synchronize()
+    # The fp64 intermediate of every sorted row.
+    off = routing.offsets.cpu().tolist()
+    st = routing.sorted_token.cpu().long()
+    f64 = torch.float64
+    y = torch.empty(m, i_dim, dtype=f64)
+    for ex in range(e):
+        r = slice(off[ex], off[ex + 1])
+        gu = (w["x_q"][st[r]].to(f64) @ w["gate_up_q"][ex].to(f64).T) * \
+            w["x_scale"][st[r]].to(f64).unsqueeze(-1) * w["gate_up_scale"][ex].to(f64)
+        y[r] = torch.nn.functional.silu(gu[:, :i_dim]) * gu[:, i_dim:]
+    _, codes_ref = orc.e8m0_block_requant(y, 128)
+    # Table position of (row, block): tile mt (256 rows per expert group, in expert order),
+    # wave block wc = r // 64, byte 2 * (r % 32) + (r % 64) // 32, one table row per block.
+    pitch = nb // (i_dim // 128)
+    table = bs.cpu().view(i_dim // 128, pitch)
+    codes = torch.empty(m, i_dim // 128, dtype=torch.long)
+    mt = 0
+    for ex in range(e):
+        for t0 in range(off[ex], off[ex + 1], 256):
+            for mm in range(t0, min(t0 + 256, off[ex + 1])):
+                r = mm - t0
+                codes[mm] = table[:, mt * 256 + (r // 64) * 64 + 2 * (r % 32) + (r % 64) // 32].long()
+            mt += 1
+    amax = y.reshape(m, -1, 128).abs().amax(-1)
+    edge = (torch.log2(amax / 448).frac().abs() < 1e-5) | (torch.log2(amax / 448).frac() > 1 - 1e-5)
+    bad = (codes != codes_ref.long()) & ~edge
+    assert int(bad.sum()) == 0, f"{int(bad.sum())} block codes differ from the rule"
+    deq = iq.cpu().to(f64).reshape(m, -1, 128) * torch.exp2(codes.to(f64) - 127).unsqueeze(-1)
+    err = (deq.reshape(m, i_dim) - y).abs()
+    sub = torch.exp2(codes.to(f64) - 127 - 10).repeat_interleave(128, 1)   # half the subnormal step
+    half_ulp = torch.maximum(y.abs() * 2.0 ** -4, sub)
+    # Values that the kernel's fp32 intermediate put on the other side of a rounding midpoint are
+    # one e4m3 step off; they must be rare.
+    # Plus the fp32 GEMM's own error, which matters where the gate or up value is a sum that
+    # cancels to almost nothing: 1e-4 of the block's absmax.
+    slack = 1e-4 * amax.repeat_interleave(128, 1)
+    assert torch.all(err <= 2 * half_ulp * 1.01 + slack)
+    assert (err > half_ulp * 1.01 + slack).double().mean().item() < 1e-2
