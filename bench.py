@@ -70,19 +70,7 @@ def run_bf16(config, steps, warmup, timer=True, router=None):
         out = kernels.moe(leaves[0], idx, leaves[1], leaves[2], leaves[3], codes)
         out.backward(dy)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    records = []
-    if timer:
-        _lib.set_timer(records)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    _lib.set_timer(None)
-    ms = (t1 - t0) * 1e3 / steps
+    ms, records, k_steps = _two_passes(step, steps, warmup, timer)
     f = flops(cfg)
     m = cfg["N"] * cfg["k"]
     mhi = m * cfg["H"] * cfg["I"]
@@ -92,7 +80,7 @@ def run_bf16(config, steps, warmup, timer=True, router=None):
     kern = {}
     for name, ts in per.items():
         avg = statistics.mean(ts)
-        d = {"ms": round(avg, 4), "calls_per_step": len(ts) // steps}
+        d = {"ms": round(avg, 4), "calls_per_step": len(ts) // k_steps}
         if name in KERNEL_MHI:
             tf = KERNEL_MHI[name] * mhi / (avg * 1e-3) / 1e12
             d.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
@@ -100,25 +88,40 @@ def run_bf16(config, steps, warmup, timer=True, router=None):
     return dict(cfg=cfg, ms=ms, tflops=f / (ms * 1e-3) / 1e12, kernels=kern, mhi=mhi)
 
 
-def _timed(fn, steps, warmup, timer=True):
+def _two_passes(fn, steps, warmup, timer=True):
+    """W untimed warmup calls, then EXACTLY `steps` timed calls between two synchronisations
+    with nothing else on the stream (the step time), then, when `timer`, a second untimed pass of
+    up to 10 calls with a HIP event pair around every library call (the per-kernel times: the
+    event records add a few microseconds between kernels, which the first pass does not pay).
+    Returns (ms per step, [(name, ev0, ev1)], calls in the event pass)."""
     import torch
     from kernels import _lib
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    records = []
-    if timer:
-        _lib.set_timer(records)
     t0 = time.perf_counter()
     for _ in range(steps):
         fn()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    _lib.set_timer(None)
+    records, k_steps = [], min(steps, 10)
+    if timer:
+        _lib.set_timer(records)
+        try:
+            for _ in range(k_steps):
+                fn()
+            torch.cuda.synchronize()
+        finally:
+            _lib.set_timer(None)
+    return (t1 - t0) * 1e3 / steps, records, k_steps
+
+
+def _timed(fn, steps, warmup, timer=True):
+    ms, records, _ = _two_passes(fn, steps, warmup, timer)
     per = {}
     for name, e0, e1 in records:
         per.setdefault(name, []).append(e0.elapsed_time(e1))
-    return (t1 - t0) * 1e3 / steps, {k: statistics.mean(v) for k, v in per.items()}
+    return ms, {k: statistics.mean(v) for k, v in per.items()}
 
 
 def run_fp8(steps, warmup):
