@@ -3,15 +3,17 @@
 // HBM bandwidth and to do nothing else expensive.
 //
 // Weights are e4m3 bytes with one E8M0 scale per 32 consecutive K values of a row (OCP MX).
-// Activations stay bf16. A workgroup owns one expert and 64 weight rows (gate/up: 32 gate rows and
-// the same 32 up rows; down: 64 rows of H); its four waves split K. Each load instruction reads
+// Activations stay bf16. A workgroup owns one expert and a few row tiles of 64 weight rows
+// (gate/up: 32 gate rows and the same 32 up rows; down: 64 rows of H). For the gate/up projection
+// (long K) its four waves split K and sum their partial accumulators through LDS; for the down
+// projection (short K) each wave runs whole row tiles of its own. Each load instruction reads
 // whole 128-byte lines of 8 rows with a nontemporal hint, a lane exchange puts each lane's 32
 // bytes of one row in place, and the lane converts them to bf16 with
 // v_cvt_scalef32_pk_bf16_fp8 (the block scale 2^(s-127) applied in the conversion, exact in
 // bf16), and feeds v_mfma_f32_16x16x32_bf16 with the expert's tokens as the other operand
-// (token rows staged in LDS: decode batches are small). The four partial accumulators are summed
-// through LDS; the gate/up kernel applies SwiGLU and writes the bf16 intermediate, the down
-// kernel writes the expert outputs, and the gate-weighted combine (moe_combine_fwd) finishes.
+// (token rows staged in LDS: decode batches are small). The gate/up kernel applies SwiGLU and
+// writes the bf16 intermediate, the down kernel writes the expert outputs, and the gate-weighted
+// combine (moe_combine_fwd) finishes.
 #include "moe_gemm_common.h"
 
 namespace moe {
