@@ -232,12 +232,23 @@ dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int
   for (int e = tid; e <= E; e += SMALL_THREADS) cnt[e] = 0;
   if (tid == 0) s_bad = 0;
   __syncthreads();
+  // Every row fits one chunk (M <= DISPATCH_CHUNK): each thread loads its PER ids once and keeps
+  // them for the scatter below.
+  constexpr int PER = DISPATCH_CHUNK / SMALL_THREADS;
+  static_assert(PER * SMALL_THREADS == DISPATCH_CHUNK, "whole rows per thread");
+  int ev[PER];
+  bool vv[PER];
   int bad = 0;
-  for (int64_t f = tid; f < M; f += SMALL_THREADS) {
-    bool valid;
-    const int e = load_expert(idx, f, E, valid);
-    atomicAdd(&cnt[e], 1);
-    bad += valid ? 0 : 1;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int64_t f = tid + (int64_t)u * SMALL_THREADS;
+    vv[u] = false;
+    ev[u] = E;
+    if (f < M) {
+      ev[u] = load_expert(idx, f, E, vv[u]);
+      atomicAdd(&cnt[ev[u]], 1);
+      bad += vv[u] ? 0 : 1;
+    }
   }
   if (bad) atomicAdd(&s_bad, bad);
   __syncthreads();
@@ -273,13 +284,16 @@ dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int
   int nbits = 0;
   while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E = invalid bucket)
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int64_t s = 0; s < M; s += SMALL_THREADS) {
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int64_t s = (int64_t)u * SMALL_THREADS;
+    if (s >= M) break;
     for (int i = tid; i < NW * (E + 1); i += SMALL_THREADS) wcnt[i / (E + 1)][i % (E + 1)] = 0;
     __syncthreads();  // also orders run[] (first step) after thread 0's scan
     const int64_t f = s + tid;
     const bool live = f < M;
-    bool valid = false;
-    const int e = live ? load_expert(idx, f, E, valid) : E;
+    const bool valid = vv[u];
+    const int e = ev[u];
     unsigned long long match = ballot64(live);
 #pragma unroll 1
     for (int bit = 0; bit < nbits; ++bit) {
