@@ -57,22 +57,26 @@ def run_bf16(config, steps, warmup, timer=True, router=None):
     import torch
     import kernels
     from kernels import _lib
-    from kernels.workloads import make_workload, flops
+    from kernels.workloads import make_workload, flops, glu_rows
 
     wl = make_workload(config, device="cuda", seed=0, scale=dict(router=router) if router else None)
     cfg = wl["cfg"]
     leaves = [wl[k].detach().requires_grad_(True) for k in ("hidden", "wt", "gate_up_proj", "down_proj")]
     idx, codes, dy = wl["idx"], wl["act_codes"], wl["grad_out"]
 
+    last = {}
+
     def step():
         for t in leaves:
             t.grad = None
         out = kernels.moe(leaves[0], idx, leaves[1], leaves[2], leaves[3], codes)
         out.backward(dy)
+        last["out"] = out
 
     ms, records, k_steps = _two_passes(step, steps, warmup, timer)
-    f = flops(cfg)
-    m = cfg["N"] * cfg["k"]
+    parity = _parity_sample(last["out"], leaves[0].grad, wl)
+    m = glu_rows(cfg, idx)
+    f = flops(m, cfg["H"], cfg["I"])
     mhi = m * cfg["H"] * cfg["I"]
     per = {}
     for name, e0, e1 in records:
@@ -85,7 +89,57 @@ def run_bf16(config, steps, warmup, timer=True, router=None):
             tf = KERNEL_MHI[name] * mhi / (avg * 1e-3) / 1e12
             d.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
         kern[name] = d
-    return dict(cfg=cfg, ms=ms, tflops=f / (ms * 1e-3) / 1e12, kernels=kern, mhi=mhi)
+    return dict(cfg=cfg, ms=ms, tflops=f / (ms * 1e-3) / 1e12, kernels=kern, mhi=mhi,
+                parity=parity, glu_rows=m)
+
+
+def _parity_sample(out, grad_hidden, wl, n_sample=256, seed=1):
+    """Checks the output and grad_hidden of the last timed step on a seeded sample of tokens
+    against the layer's fp32 math: the library's pure-PyTorch moe_eager (the reference's eager
+    algorithm, kernels/sm75/moe.py:884-909) in fp32 with autograd, on the sampled tokens only
+    (a token's output and input gradient depend on its own row alone). Gate: max|d| / max|ref| <
+    1.5e-2 per tensor, the reference bench's pass rule (/root/reference/bench.py:151-163)."""
+    import torch
+    import kernels
+    n = wl["hidden"].shape[0]
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    rows = torch.randperm(n, generator=g)[:min(n_sample, n)].sort().values.to(out.device)
+    x = wl["hidden"][rows].float().requires_grad_(True)
+    ref = kernels.moe_eager(x, wl["idx"][rows], wl["wt"][rows].float(),
+                            wl["gate_up_proj"].float(), wl["down_proj"].float(), wl["act_codes"])
+    ref.backward(wl["grad_out"][rows].float())
+    res = {}
+    for name, mine, truth in (("out", out[rows], ref), ("grad_hidden", grad_hidden[rows], x.grad)):
+        d = (mine.float() - truth).abs().max().item()
+        res[name] = round(d / (truth.abs().max().item() + 1e-12), 6)
+    res["tokens_checked"] = int(rows.numel())
+    res["parity_ok"] = all(v < 1.5e-2 for k, v in res.items() if k in ("out", "grad_hidden"))
+    return res
+
+
+# The reference's published fwd+bwd times of its MoE stack (bf16, N=16384, H=512, I=768, k=2) on an
+# RTX PRO 6000 (Blackwell): its grouped path and its per-expert path, 32 GLU experts
+# (/root/reference/.autoresearch/moe_grouped_results.jsonl:23). Other hardware: context only.
+REF_STACK_MS = {"grouped_cublas_polyglu": 3.526, "per_expert": 8.864, "E_glu": 32,
+                "gpu": "RTX PRO 6000 Blackwell"}
+
+
+def run_stack(name, steps, warmup):
+    """The reference bench_moe stack (PolyGLU codes i % 3 with NormSiLU, plus Identity and Zero):
+    bf16 fwd+bwd of kernels.moe, step time, TFLOP/s over the GLU-routed rows (18*M_glu*H*I), the
+    per-kernel times and the sampled parity check."""
+    r = run_bf16(name, steps, warmup)
+    cfg = r["cfg"]
+    out = {"ms_per_step": round(r["ms"], 4), "tflops": round(r["tflops"], 2),
+           "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4), "glu_rows": r["glu_rows"],
+           "kernels_ms": {k: v["ms"] for k, v in r["kernels"].items()}, "parity": r["parity"],
+           "workload": (f"{name}: bf16 fwd+bwd N={cfg['N']} H={cfg['H']} I={cfg['I']} "
+                        f"codes={cfg['codes']} k={cfg['k']} (reference bench.py:617-631 shape)")}
+    if cfg["E"] - 2 == REF_STACK_MS["E_glu"]:
+        out["reference_published_context"] = dict(REF_STACK_MS, note=(
+            "the reference's own published times for this stack size on other hardware; context, "
+            "not a target"))
+    return out
 
 
 def _two_passes(fn, steps, warmup, timer=True):
@@ -125,14 +179,19 @@ def _timed(fn, steps, warmup, timer=True):
 
 
 def run_fp8(steps, warmup):
-    """Config 4: fp8 forward; FLOPs 6*M*H*I over the routed rows."""
+    """Config 4: fp8 forward from bf16 activations (per-token e4m3 quantisation of x, then the
+    fp8 layer); FLOPs 6*M*H*I over the routed rows."""
     import kernels
+    from kernels.gfx950.lowp import rowquant_fp8
     from kernels.workloads import make_workload, flops
     w = make_workload(4, device="cuda", seed=0)
     cfg = w["cfg"]
-    args = (w["x_q"], w["x_scale"], w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"],
-            w["down_q"], w["down_scale"])
-    ms, kern = _timed(lambda: kernels.moe_fp8(*args), steps, warmup)
+    args = (w["idx"], w["wt"], w["gate_up_q"], w["gate_up_scale"], w["down_q"], w["down_scale"])
+
+    def step():   # a caller holds bf16 activations: the per-token quantisation is in the step
+        x_q, x_scale = rowquant_fp8(w["hidden"])
+        return kernels.moe_fp8(x_q, x_scale, *args)
+    ms, kern = _timed(step, steps, warmup)
     f = flops(cfg, backward=False)
     call = kern.get("moe_fp8_fwd")
     return {"tflops": round(f / (ms * 1e-3) / 1e12, 2), "ms_per_step": round(ms, 4),
@@ -140,8 +199,9 @@ def run_fp8(steps, warmup):
             "gemm_call_ms": round(call, 4) if call else None,
             "gemm_call_tflops": round(f / (call * 1e-3) / 1e12, 1) if call else None,
             "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
-            "workload": (f"{cfg['name']}: fp8-e4m3 fwd N={cfg['N']} H={cfg['H']} I={cfg['I']} "
-                         f"E={cfg['E']} k={cfg['k']}, peak {PEAK_FP8_TFLOPS} TFLOP/s")}
+            "workload": (f"{cfg['name']}: bf16 x -> per-token e4m3 quantisation -> fp8-e4m3 fwd "
+                         f"N={cfg['N']} H={cfg['H']} I={cfg['I']} E={cfg['E']} k={cfg['k']}, "
+                         f"peak {PEAK_FP8_TFLOPS} TFLOP/s")}
 
 
 def run_mxfp8(steps, warmup):
@@ -370,7 +430,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--config", type=lambda v: int(v) if v.isdigit() else v, default=3,
+                    help="1-5, or bench_moe_stack / bench_moe_stack_e32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
@@ -425,6 +486,7 @@ def main():
                    "global_batch": cfg["N"], "seq_len": None, "parallelism": "single GPU"},
         "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline, "kernels": kern,
+        "parity": r["parity"], "parity_ok": r["parity"]["parity_ok"],
     }
     if not args.no_extra:
         other = 2 if args.config != 2 else 3
@@ -432,7 +494,11 @@ def main():
         r2 = run_bf16(other, max(5, args.steps // 2), 2, timer=False)
         line["extra_configs"] = {r2["cfg"]["name"]: {"tflops": round(r2["tflops"], 2),
                                                      "ms_per_step": round(r2["ms"], 4),
-                                                     "frac_of_peak": round(r2["tflops"] / PEAK_BF16_TFLOPS, 4)}}
+                                                     "frac_of_peak": round(r2["tflops"] / PEAK_BF16_TFLOPS, 4),
+                                                     "parity": r2["parity"]}}
+        for stack in ("bench_moe_stack", "bench_moe_stack_e32"):
+            _log(f"extra {stack} (the reference bench's PolyGLU stack; unfused GLU path)")
+            line["extra_configs"][stack] = run_stack(stack, max(10, args.steps), 3)
         _log("extra config 4 (fp8 fwd)")
         line["extra_configs"]["fp8_fwd"] = run_fp8(max(5, args.steps // 2), 2)
         _log("extra config 5 (MXFP8 decode)")

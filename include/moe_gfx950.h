@@ -53,7 +53,9 @@ size_t moe_get_workspace_size(int64_t n_tokens, int top_k, int n_experts);
  * prefix of ceil(counts/moe_tile_rows())), expert_order[E] (expert ids by descending count, ties
  * by id), sorted_token[M] (token id t of each sorted row),
  * sorted_flat[M] (flat index t*k+j of each sorted row), flat_to_sorted[M] (inverse permutation;
- * -1 for an index outside [0, E)), status[0] += number of such out-of-range indices. */
+ * -1 for an index outside [0, E)), status[0] += number of such out-of-range indices. Such indices
+ * are dropped, so only offsets[E] <= M rows are routed: sorted_token and sorted_flat hold -1 at
+ * positions [offsets[E], M). */
 int moe_dispatch(const int64_t* top_k_indices, int64_t n_tokens, int top_k, int n_experts,
                  int32_t* counts, int32_t* offsets, int32_t* tile_offsets, int32_t* expert_order,
                  int32_t* sorted_token, int32_t* sorted_flat, int32_t* flat_to_sorted,
@@ -118,7 +120,9 @@ int moe_combine_fwd(int dtype, const void* eo, const void* hidden, const void* t
 
 /* Combine backward: grad_eo[m] = grad_out[t] * w (GLU rows), grad_wt[flat] = sum_h grad_out[t,h] *
  * row[h] (fp32 reduction; row = eo[m] for GLU, hidden[t] for Identity, 0 for Zero).
- * grad_out rows are `grad_out_ld` elements apart. Replaces `_combine_bwd`
+ * grad_out rows are `grad_out_ld` elements apart. Sorted rows with sorted_flat = -1 (past the
+ * routed count) are skipped; grad_wt entries of dropped slots are left as the caller set them.
+ * Replaces `_combine_bwd`
  * (kernels/sm75/moe.py:688-701,712-720) and the grouped bwd prologue (:606-608,616-617). */
 int moe_combine_bwd(int dtype, const void* grad_out, int64_t grad_out_ld, const void* eo,
                     const void* hidden, const void* top_k_weights, const int64_t* top_k_indices,

@@ -144,3 +144,24 @@ def test_moe_eager_matches_oracle_on_cpu():
     a = kernels.moe_eager(x, idx, wt, gu, dw, torch.tensor(codes, dtype=torch.int32), ap)
     b = orc.moe_forward(x, idx, wt, gu, dw, codes, ap)
     torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
+def test_row_expert_with_dropped_ids():
+    """Per-sorted-row expert ids from the dispatch offsets when out-of-range ids leave fewer routed
+    rows than N*k: rows past offsets[E] get E (no expert), the per-row gathers clamp it and the
+    SiTU-parameter scatter masks it."""
+    from kernels.gfx950.moe import _Routing, _row_params
+    # routing [[0, 2], [-1, 2], [2, 5], [1, 0]] over 4 experts: ids -1 and 5 are dropped
+    n_exp = 4
+    offsets = torch.tensor([0, 2, 3, 6, 6], dtype=torch.int32)   # counts 2, 1, 3, 0
+    r = _Routing.__new__(_Routing)
+    r.offsets = offsets
+    rexp = r.row_expert(n_exp, 8)
+    assert rexp.tolist() == [0, 0, 1, 2, 2, 2, 4, 4]
+    codes_t = torch.tensor([5, 2, 5, 3], dtype=torch.int32)
+    ap = torch.tensor([[2.0, 3.0], [4.0, 5.0], [6.0, 7.0], [8.0, 9.0]])
+    row_act, ra, rg, rexp2 = _row_params(r, codes_t, ap, n_exp, 8)
+    assert row_act.tolist() == [5, 5, 2, 5, 5, 5, 3, 3]
+    assert ra.tolist() == [2, 2, 4, 6, 6, 6, 8, 8] and rg.tolist() == [3, 3, 5, 7, 7, 7, 9, 9]
+    valid = rexp2 < min(ap.shape[0], n_exp)
+    assert valid.tolist() == [True] * 6 + [False] * 2

@@ -31,6 +31,9 @@ def _check(idx_cpu, n_experts):
     np.testing.assert_array_equal(r.sorted_flat.cpu().numpy()[:n_valid], ref["sorted_flat"])
     np.testing.assert_array_equal(r.sorted_token.cpu().numpy()[:n_valid], ref["sorted_token"])
     np.testing.assert_array_equal(r.flat_to_sorted.cpu().numpy()[:m], ref["flat_to_sorted"])
+    # positions past the routed count (dropped ids) hold -1
+    assert (r.sorted_flat.cpu().numpy()[n_valid:m] == -1).all()
+    assert (r.sorted_token.cpu().numpy()[n_valid:m] == -1).all()
     assert int(r.status.item()) == int((ref["flat_to_sorted"] < 0).sum())
     return r
 

@@ -279,3 +279,27 @@ def test_bf16_out_of_range_expert_ids():
     ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, dtype=torch.float64)
     mine = _run(kernels.moe, *[t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)])
     _assert_bf16(mine, ref, (hid, idx, w, gu, dw, go), codes)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_unfused_codes_out_of_range_expert_ids(dtype):
+    """Unfused codes (RMS-normalised 2/6/7, SiTU 5 with act_params) plus an Identity slot, with
+    ids of -1 and >= E in the routing: the routed rows are fewer than N*k, so the per-row code and
+    SiTU-parameter gathers run past the routed count. Dropped ids add nothing, as the reference's
+    mask drops them (kernels/sm75/moe.py:895-899)."""
+    codes = [2, 5, 6, 7, 0, 3]
+    hid, idx, w, gu, dw, codes_t, ap, go = _case(codes, 5, dtype=dtype, n=400, h=128, i=96, k=3,
+                                                 seed=11)
+    idx[::5, 0] = 6
+    idx[::9, 1] = -1
+    idx[::13, 2] = 1000
+    _say(f"{dtype} unfused codes with out-of-range ids")
+    ref = orc.moe_fwd_bwd(hid, idx, w, gu, dw, codes, go, act_params=ap, dtype=torch.float64)
+    dev = [t.cuda() for t in (hid, idx, w, gu, dw, codes_t, go)]
+    mine = _run(kernels.moe_per_expert, *dev, ap=ap.cuda())
+    if dtype == torch.float32:
+        _assert_fp32(mine, ref, keys=GRADS + ("grad_act_params",))
+    else:
+        eager = eager_16bit(orc, hid, idx, w, gu, dw, codes, go, dtype, act_params=ap)
+        assert_16bit_parity(mine, ref, eager, GRADS)
+        assert _rel(mine["grad_act_params"], ref["grad_act_params"]) < 3e-2

@@ -67,10 +67,10 @@ def test_split_matches_unsplit_is_deterministic_and_clears_counters(which):
         d = (got.float() - ref).abs()
         assert bool(torch.isfinite(got).all())
         assert (d <= 1e-2 * ref.abs() + 1e-2).all(), d.max().item()
-    # the split and unsplit sums differ only by fp32 summation order before the bf16 store; some
-    # of the ~10^6 outputs round differently, which shows the split path ran
-    assert not torch.equal(s1, plain)
+    # the split and unsplit sums differ only by fp32 summation order before the bf16 store
     assert ((s1.float() - plain.float()).abs() <= 2 ** -7 * plain.float().abs() + 1e-3).all()
     n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+    # the split path ran: its fp32 partial sums were written into the (zeroed) workspace
+    assert bool(ws[: n_cus * 65536 * 4].view(torch.int32).ne(0).any())
     counters = ws[n_cus * 65536 * 4:].view(torch.int32)
     assert int(counters.abs().sum()) == 0

@@ -374,7 +374,10 @@ def test_workload_routing_properties():
         assert idx.shape == (512, k) and idx.dtype == torch.int64
         assert int(idx.min()) >= 0 and int(idx.max()) < e
         assert torch.all(idx.sort(-1).values.diff(dim=-1) > 0)          # distinct experts per token
-        torch.testing.assert_close(wt.float().sum(-1), torch.ones(512), rtol=1e-2, atol=1e-2)
+        if w["cfg"]["router"] == "stack_softmax":   # the reference bench keeps softmax top-k gates
+            assert bool((wt.float().sum(-1) < 1).all()) and bool((wt > 0).all())
+        else:
+            torch.testing.assert_close(wt.float().sum(-1), torch.ones(512), rtol=1e-2, atol=1e-2)
 
 
 def test_zipf_config_has_empty_and_full_experts():

@@ -127,7 +127,8 @@ __device__ __forceinline__ void stg16(void* p, i32x4 v) { *(i32x4*)p = v; }
 __device__ __forceinline__ i32x4 zero4() { return i32x4{0, 0, 0, 0}; }
 
 // sigma(g) = 1 / (1 + e^-g) with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE
-// division sequence; e^-g = inf gives 0, so silu(-inf..) -> -0 as with a division.
+// division sequence. A large negative finite g gives e^-g = inf, sigma = 0 and silu = -0; g = -inf
+// gives silu = -inf * 0 = NaN, the same as with a division.
 __device__ __forceinline__ float sigmoid(float g) {
   return __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }

@@ -55,6 +55,20 @@ __device__ __forceinline__ int load_expert(const int64_t* idx, int64_t f, int E,
   return valid ? (int)v : E;
 }
 
+// Writes -1 to sorted_token / sorted_flat at the positions of [f0, f0 + n) that lie in
+// [routed, M): the tail of the sorted arrays when some ids were dropped (out of range), so a
+// kernel walking all M sorted rows finds no stale indices there.
+__device__ __forceinline__ void fill_tail(int64_t f0, int n, int nthreads, int routed, int64_t M,
+                                          int32_t* sorted_token, int32_t* sorted_flat) {
+  for (int i = threadIdx.x; i < n; i += nthreads) {
+    const int64_t p = f0 + i;
+    if (p >= routed && p < M) {
+      sorted_token[p] = -1;
+      sorted_flat[p] = -1;
+    }
+  }
+}
+
 __global__ void __launch_bounds__(DISPATCH_THREADS)
 dispatch_hist_kernel(const int64_t* __restrict__ idx, int64_t M, int E, int32_t* __restrict__ hist,
                      int32_t* __restrict__ status) {
@@ -170,6 +184,9 @@ dispatch_scatter_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, i
   while ((1 << nbits) <= E) ++nbits;  // ids 0..E (E = invalid bucket)
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
   const int64_t f0 = (int64_t)b * DISPATCH_CHUNK;
+  // Sorted positions past the routed count (one per dropped id) hold -1: this chunk's share of
+  // [offsets[E], M) is its own index range, which no valid row's position reaches.
+  fill_tail(f0, DISPATCH_CHUNK, DISPATCH_THREADS, offsets[E], M, sorted_token, sorted_flat);
   for (int s = 0; s < DISPATCH_CHUNK; s += DISPATCH_THREADS) {
     for (int i = threadIdx.x; i < NW * (E + 1); i += DISPATCH_THREADS) wcnt[i / (E + 1)][i % (E + 1)] = 0;
     __syncthreads();
@@ -269,6 +286,7 @@ dispatch_small_kernel(const int64_t* __restrict__ idx, int64_t M, int top_k, int
       tile_offsets[E] = t_tot;
       if (s_bad) atomicAdd(status, s_bad);
     }
+    fill_tail(0, DISPATCH_CHUNK, SMALL_THREADS, o_tot, M, sorted_token, sorted_flat);
   }
   // Experts by descending count (ties by id).
   for (int e = tid; e < E; e += SMALL_THREADS) {

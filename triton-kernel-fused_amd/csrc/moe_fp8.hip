@@ -71,6 +71,9 @@ fp8_gemm_kernel(Fp8Args a) {
     const fp8e4m3* Pe = a.P + (size_t)t.e * a.p_e;
     lq.init(wc * v4::WQ);
     if constexpr (!GLU) {
+      // The gate/up epilogue writes scale codes only for rows below its group end, so the bytes
+      // of a tail tile's rows past m_end are stale; they scale only accumulator rows that the
+      // epilogue does not store.
       lq.sp = (const char*)a.q_bscale + (size_t)t.mt * v4::TILE + wc * v4::WQ +
               2 * (v4::lane_id() & 31);
       lq.s_ld = a.bs_ld;

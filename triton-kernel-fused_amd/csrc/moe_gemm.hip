@@ -1283,7 +1283,7 @@ static int device_cus() {
   return n;
 }
 
-// 256x256 token GEMMs: the persistent ring kernel (up to 64 GLU experts, no K split), else the
+// 256x256 token GEMMs: the persistent ring kernel (any expert count, no K split), else the
 // one-tile-per-workgroup ring kernel when K is a multiple of its 64-value step, otherwise (dX
 // GEMMs with K a multiple of 32) the four-wave five-stage kernel.
 template <typename T, int EPI, bool P_RC>

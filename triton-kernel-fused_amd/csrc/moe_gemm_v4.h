@@ -502,7 +502,7 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
 // Expert lookup of token tiles from the sorted-row offsets, in scalar registers: a walk over the
 // experts that resumes where the previous lookup stopped (a workgroup's token tiles come in
 // non-decreasing order when its tile stride is a multiple of the tile group; otherwise the walk
-// restarts). The offsets are read with scalar loads (scalar cache, counted apart from the vector
+// steps back from where it is). The offsets are read with scalar loads (scalar cache, counted apart from the vector
 // memory operations whose waits the ring relies on).
 struct Experts {
   const int32_t* off;
@@ -527,11 +527,15 @@ struct Experts {
   }
   // Expert of token tile mt (< n_mt) and its rows [m0, m_end).
   __device__ __forceinline__ void lookup(int mt, int& ex, int& m0, int& m_end) {
-    if (mt < pref) {
-      e = 0;
-      pref = 0;
-    }
     int o0 = v3::sload(off + e), o1 = v3::sload(off + e + 1);
+    // With tile groups a workgroup's token tiles can step back by up to a group: walk back
+    // from the current expert rather than restarting at expert 0 (O(distance), not O(E)).
+    while (mt < pref) {
+      --e;
+      o1 = o0;
+      o0 = v3::sload(off + e);
+      pref -= (o1 - o0 + TILE - 1) / TILE;
+    }
     while (mt >= pref + (o1 - o0 + TILE - 1) / TILE) {
       pref += (o1 - o0 + TILE - 1) / TILE;
       ++e;

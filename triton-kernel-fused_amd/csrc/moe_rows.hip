@@ -167,6 +167,7 @@ combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
 }
 
 // Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
+// Rows past the routed count carry t = f = -1 (dispatch) and are skipped.
 template <typename T>
 __global__ void __launch_bounds__(ROW_THREADS)
 combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict__ eo,
@@ -180,6 +181,7 @@ combine_bwd_kernel(const T* __restrict__ go, int64_t go_ld, const T* __restrict_
   const int lane = threadIdx.x & 63;
   const int t = st[r];
   const int f = sflat[r];
+  if (f < 0 || t < 0) return;  // past the routed count (dropped ids): no slot
   const int kind = slot_kind(idx[f], codes, E_glu, E_all, 0);
   const float w = to_f32(wt[f]);
   float dot = 0.f;

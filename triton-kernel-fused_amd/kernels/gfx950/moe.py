@@ -135,9 +135,12 @@ class _Routing:
             raise ValueError(f"{int(self.status.item())} top_k_indices outside [0, {n_experts})")
 
     def row_expert(self, n_experts, m):
-        """Expert id of every sorted row (device op, no host sync)."""
-        return torch.repeat_interleave(torch.arange(n_experts, device=self.counts.device),
-                                       self.counts, output_size=m)
+        """Expert id of every sorted row (device op, no host sync): the e with
+        offsets[e] <= r < offsets[e+1]. Rows past the routed count offsets[E] (there are fewer than
+        N*k routed rows when some ids lie outside [0, E), which dispatch drops) get the value
+        n_experts, which indexes nothing: callers clamp it for gathers and mask it for scatters."""
+        rows = torch.arange(m, device=self.offsets.device, dtype=torch.int32)
+        return torch.searchsorted(self.offsets[1:n_experts + 1], rows, right=True)
 
 
 def dispatch(top_k_indices, n_experts):
@@ -146,14 +149,18 @@ def dispatch(top_k_indices, n_experts):
 
 
 def _row_params(routing, codes_t, ap32, n_experts, m):
-    """Per sorted row: act code, SiTU alpha/gamma (or None) and expert id (unfused GLU path)."""
+    """Per sorted row: act code, SiTU alpha/gamma (or None) and expert id (unfused GLU path).
+    The returned expert id is n_experts for rows past the routed count; the per-row gathers here
+    read a clamped copy (those rows are computed by the row kernels but never read downstream)."""
     rexp = routing.row_expert(n_experts, m)
-    row_act = codes_t.to(torch.int32).index_select(0, rexp).contiguous()
+    rclamp = rexp.clamp(max=max(n_experts - 1, 0))
+    row_act = codes_t.to(torch.int32).index_select(0, rclamp).contiguous()
     if ap32 is not None:
         ap_full = torch.ones(n_experts, 2, device=ap32.device, dtype=torch.float32)
-        ap_full[: ap32.shape[0]] = ap32[:n_experts]
-        row_alpha = ap_full[:, 0].index_select(0, rexp).contiguous()
-        row_gamma = ap_full[:, 1].index_select(0, rexp).contiguous()
+        n_ap = min(ap32.shape[0], n_experts)
+        ap_full[:n_ap] = ap32[:n_ap]
+        row_alpha = ap_full[:, 0].index_select(0, rclamp).contiguous()
+        row_gamma = ap_full[:, 1].index_select(0, rclamp).contiguous()
     else:
         row_alpha = row_gamma = None
     return row_act, row_alpha, row_gamma, rexp
@@ -294,7 +301,7 @@ class _MoEFunction(torch.autograd.Function):
                               _lib.ptr(dg), stream)
                     if need_ap:
                         g_ap = torch.zeros(ap32.shape[0], 2, device=dev, dtype=torch.float32)
-                        valid = rexp < ap32.shape[0]
+                        valid = rexp < min(ap32.shape[0], n_exp)   # routed rows only
                         g_ap[:, 0].index_add_(0, rexp[valid], da[valid])
                         g_ap[:, 1].index_add_(0, rexp[valid], dg[valid])
             if need_dw:
