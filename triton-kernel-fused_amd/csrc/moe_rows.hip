@@ -16,8 +16,8 @@ template <typename T> struct Vec8;  // 16 bytes of T as floats
 template <> struct Vec8<bf16> {
   static constexpr int N = 8;
   // bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 bits.
-  __device__ __forceinline__ static void ld(const bf16* p, float* v) {
-    const uint4 u = *(const uint4*)p;
+  __device__ __forceinline__ static void ld(const bf16* p, float* v) { cvt(*(const uint4*)p, v); }
+  __device__ __forceinline__ static void cvt(const uint4& u, float* v) {
     const unsigned w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -38,8 +38,8 @@ template <> struct Vec8<bf16> {
 template <> struct Vec8<f16> {
   static constexpr int N = 8;
   typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 h2;
-  __device__ __forceinline__ static void ld(const f16* p, float* v) {
-    const uint4 u = *(const uint4*)p;
+  __device__ __forceinline__ static void ld(const f16* p, float* v) { cvt(*(const uint4*)p, v); }
+  __device__ __forceinline__ static void cvt(const uint4& u, float* v) {
     const unsigned w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -62,6 +62,10 @@ template <> struct Vec8<float> {
   __device__ __forceinline__ static void ld(const float* p, float* v) {
     f32x4 u = *(const f32x4*)p;
     v[0] = u[0]; v[1] = u[1]; v[2] = u[2]; v[3] = u[3];
+  }
+  __device__ __forceinline__ static void cvt(const uint4& u, float* v) {
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y);
+    v[2] = __uint_as_float(u.z); v[3] = __uint_as_float(u.w);
   }
   __device__ __forceinline__ static void st(float* p, const float* v) {
     *(f32x4*)p = f32x4{v[0], v[1], v[2], v[3]};
@@ -402,6 +406,194 @@ glu_bwd_kernel(const T* __restrict__ go_, int64_t go_rs, int64_t go_cs, const T*
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Row-wise PolyGLU, vector form: one wave per row and 16-byte loads and stores (V elements per
+// lane and chunk), for rows whose element offsets are multiples of V and 16-byte aligned. A lane
+// keeps chunks lane, lane + 64, ... (up to NJ of them, NJ * 64 * V >= I) in registers, so the RMS
+// pass of codes 2/6/7 and the main pass read each element once, and every reduction is a wave
+// reduction (no block barrier; a wave past the last row leaves at once). The per-element math is
+// the scalar kernels' above.
+constexpr int GLU_VEC_WAVES = 4;
+
+// act(gate) and act'(gn) of the codes (the derivative with respect to the normalised gate gn for
+// 2/6/7, to gate otherwise; code 5's pieces are computed by the callers).
+__device__ __forceinline__ void glu_row_act_dact(int code, float gn, float sig, float& act,
+                                                 float& df) {
+  if (code == 1 || code == 6) {
+    const float rl = fmaxf(gn, 0.f);
+    act = rl * rl;
+    df = 2.f * rl;
+  } else if (code == 7) {
+    const float tg = tanh_via_sigmoid(gn);
+    act = tg * sig;
+    df = (1.f - tg * tg) * sig + tg * sig * (1.f - sig);
+  } else {  // 0, 2 (and any other code, as the scalar kernels)
+    act = gn * sig;
+    df = sig * (1.f + gn * (1.f - sig));
+  }
+}
+
+template <typename T, int NJ>
+__global__ void __launch_bounds__(64 * GLU_VEC_WAVES)
+glu_fwd_vec_kernel(const T* __restrict__ gu, int64_t gu_ld, const int32_t* __restrict__ row_act,
+                   const float* __restrict__ alpha, const float* __restrict__ gamma,
+                   int ap_stride, int64_t n_rows, int I, T* __restrict__ out, int64_t out_ld) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t row = (int64_t)blockIdx.x * GLU_VEC_WAVES + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int nch = I / V;
+  const T* g = gu + row * gu_ld;
+  const T* u = g + I;
+  const int code = row_act[row];
+  const float aa = alpha ? alpha[row * ap_stride] : 1.f;
+  const float gg = gamma ? gamma[row * ap_stride] : 1.f;
+  // The row's chunks stay packed in registers (16 bytes each) and are unpacked where used.
+  uint4 graw[NJ], uraw[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    graw[j] = uraw[j] = uint4{0u, 0u, 0u, 0u};
+    if (c < nch) {
+      graw[j] = *(const uint4*)(g + c * V);
+      uraw[j] = *(const uint4*)(u + c * V);
+    }
+  }
+  float rinv = 1.f;
+  if (is_norm_code(code)) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float gv[V];
+      Vec8<T>::cvt(graw[j], gv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += gv[i] * gv[i];
+    }
+    ss = wave_sum(ss);
+    rinv = 1.f / sqrtf(ss / I + NS_EPS);
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    if (c >= nch) continue;
+    float o[V], gv[V], uv[V];
+    Vec8<T>::cvt(graw[j], gv);
+    Vec8<T>::cvt(uraw[j], uv);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float gate = gv[i];
+      const float gn = is_norm_code(code) ? gate * rinv : gate;
+      const float sig = sigmoid(gn);
+      float act, df;
+      if (code == 5) act = gg * tanh_via_sigmoid(aa * gate) * sig;
+      else glu_row_act_dact(code, gn, sig, act, df);
+      o[i] = act * uv[i];
+    }
+    Vec8<T>::st(out + row * out_ld + c * V, o);
+  }
+}
+
+template <typename T, int NJ>
+__global__ void __launch_bounds__(64 * GLU_VEC_WAVES)
+glu_bwd_vec_kernel(const T* __restrict__ go_, int64_t go_rs, const T* __restrict__ gu,
+                   int64_t gu_ld, const int32_t* __restrict__ row_act,
+                   const float* __restrict__ alpha, const float* __restrict__ gamma,
+                   int ap_stride, int64_t n_rows, int I, T* __restrict__ ggu, int64_t ggu_ld,
+                   float* __restrict__ da, float* __restrict__ dg) {
+  constexpr int V = Vec8<T>::N;
+  const int64_t row = (int64_t)blockIdx.x * GLU_VEC_WAVES + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int nch = I / V;
+  const T* g = gu + row * gu_ld;
+  const T* u = g + I;
+  const T* gop = go_ + row * go_rs;
+  const int code = row_act[row];
+  const bool norm = is_norm_code(code);
+  const float aa = alpha ? alpha[row * ap_stride] : 1.f;
+  const float gg = gamma ? gamma[row * ap_stride] : 1.f;
+  uint4 graw[NJ], uraw[NJ], oraw[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    graw[j] = uraw[j] = oraw[j] = uint4{0u, 0u, 0u, 0u};
+    if (c < nch) {
+      graw[j] = *(const uint4*)(g + c * V);
+      uraw[j] = *(const uint4*)(u + c * V);
+      oraw[j] = *(const uint4*)(gop + c * V);
+    }
+  }
+  float r = 1.f, rinv = 1.f, S = 0.f;
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float gv[V];
+      Vec8<T>::cvt(graw[j], gv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) ss += gv[i] * gv[i];
+    }
+    ss = wave_sum(ss);
+    r = sqrtf(ss / I + NS_EPS);
+    rinv = 1.f / r;
+    float sacc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      float gv[V], uv[V], ov[V];
+      Vec8<T>::cvt(graw[j], gv);
+      Vec8<T>::cvt(uraw[j], uv);
+      Vec8<T>::cvt(oraw[j], ov);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float gn = gv[i] * rinv;
+        float act, df;
+        glu_row_act_dact(code, gn, sigmoid(gn), act, df);
+        sacc += ov[i] * uv[i] * df * gn;  // zero-filled chunks add nothing
+      }
+    }
+    S = wave_sum(sacc);
+  }
+  float sda = 0.f, sdg = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    if (c >= nch) continue;
+    float dgt[V], dup[V], gv[V], uv[V], ov[V];
+    Vec8<T>::cvt(graw[j], gv);
+    Vec8<T>::cvt(uraw[j], uv);
+    Vec8<T>::cvt(oraw[j], ov);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float gate = gv[i];
+      const float gn = norm ? gate * rinv : gate;
+      const float sig = sigmoid(gn);
+      const float gup = ov[i] * uv[i];
+      float act, df;
+      if (code == 5) {
+        const float t5 = tanh_via_sigmoid(aa * gate);
+        act = gg * t5 * sig;
+        dgt[i] = gup * gg * (aa * (1.f - t5 * t5) * sig + t5 * sig * (1.f - sig));
+        sda += gup * gg * gate * (1.f - t5 * t5) * sig;
+        sdg += gup * t5 * sig;
+      } else {
+        glu_row_act_dact(code, gn, sig, act, df);
+        dgt[i] = norm ? (gup * df - (S / I) * gn) / r : gup * df;
+      }
+      dup[i] = ov[i] * act;
+    }
+    Vec8<T>::st(ggu + row * ggu_ld + c * V, dgt);
+    Vec8<T>::st(ggu + row * ggu_ld + I + c * V, dup);
+  }
+  if (da) {
+    sda = wave_sum(sda);
+    sdg = wave_sum(sdg);
+    if (lane == 0) {
+      da[row] = code == 5 ? sda : 0.f;
+      dg[row] = code == 5 ? sdg : 0.f;
+    }
+  }
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -448,6 +640,16 @@ static int check_rows(int dtype, int64_t n, int top_k, int64_t H, int n_experts,
 }
 
 static unsigned row_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
+
+// Register chunks per lane of the vector GLU kernels (1, 2, 4 ... max_nj: I <= 64 * NJ * v), or 0
+// when I is not a multiple of the vector width v or too long (the scalar kernels then run).
+static int glu_vec_chunks(int64_t I, int v, int max_nj) {
+  if (I % v) return 0;
+  const int64_t nch = I / v;
+  for (int nj = 1; nj <= max_nj; nj *= 2)
+    if (nch <= 64 * nj) return nj;
+  return 0;
+}
 
 // Waves per token for the per-token gathers (combine, un-permute): one per 64*vec-column chunk.
 // Each wave keeps its token's 8 row loads in flight together; whole-token waves loading one row
@@ -570,9 +772,23 @@ extern "C" int moe_glu_fwd(int dtype, const void* gate_up, int64_t gu_ld, const 
   if (!gate_up || !row_act || !out || n_rows >= (1ll << 31)) return MOE_ERR_SHAPE;
   if ((alpha == nullptr) != (gamma == nullptr)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  MOE_BY_DTYPE(dtype, glu_fwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
-               (const T_*)gate_up, gu_ld, row_act, alpha, gamma, ap_stride, (int)I, (T_*)out,
-               out_ld);
+  const int v = vec_of(dtype);
+  const int nj = glu_vec_chunks(I, v, 8);
+  if (nj && gu_ld % v == 0 && out_ld % v == 0 && al16(gate_up) && al16(out)) {
+    const dim3 grid((unsigned)((n_rows + GLU_VEC_WAVES - 1) / GLU_VEC_WAVES)), block(64 * GLU_VEC_WAVES);
+#define MOE_GLU_FWD_VEC(NJ_)                                                                     \
+  MOE_BY_DTYPE_B(dtype, glu_fwd_vec_kernel, NJ_, grid, block, s, (const T_*)gate_up, gu_ld,     \
+                 row_act, alpha, gamma, ap_stride, n_rows, (int)I, (T_*)out, out_ld)
+    if (nj == 1) MOE_GLU_FWD_VEC(1);
+    else if (nj == 2) MOE_GLU_FWD_VEC(2);
+    else if (nj == 4) MOE_GLU_FWD_VEC(4);
+    else MOE_GLU_FWD_VEC(8);
+#undef MOE_GLU_FWD_VEC
+  } else {
+    MOE_BY_DTYPE(dtype, glu_fwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
+                 (const T_*)gate_up, gu_ld, row_act, alpha, gamma, ap_stride, (int)I, (T_*)out,
+                 out_ld);
+  }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -588,9 +804,25 @@ extern "C" int moe_glu_bwd(int dtype, const void* grad_out, int64_t go_row_strid
   if ((alpha == nullptr) != (gamma == nullptr) || (da_out == nullptr) != (dg_out == nullptr))
     return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  MOE_BY_DTYPE(dtype, glu_bwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
-               (const T_*)grad_out, go_row_stride, go_col_stride, (const T_*)gate_up, gu_ld,
-               row_act, alpha, gamma, ap_stride, (int)I, (T_*)ggu_out, ggu_ld, da_out, dg_out);
+  const int v = vec_of(dtype);
+  // At most 4 chunks per lane: the backward holds three rows' worth (gate, up, grad).
+  const int nj = glu_vec_chunks(I, v, 4);
+  if (nj && go_col_stride == 1 && go_row_stride % v == 0 && gu_ld % v == 0 && ggu_ld % v == 0 &&
+      al16(grad_out) && al16(gate_up) && al16(ggu_out)) {
+    const dim3 grid((unsigned)((n_rows + GLU_VEC_WAVES - 1) / GLU_VEC_WAVES)), block(64 * GLU_VEC_WAVES);
+#define MOE_GLU_BWD_VEC(NJ_)                                                                     \
+  MOE_BY_DTYPE_B(dtype, glu_bwd_vec_kernel, NJ_, grid, block, s, (const T_*)grad_out,           \
+                 go_row_stride, (const T_*)gate_up, gu_ld, row_act, alpha, gamma, ap_stride,    \
+                 n_rows, (int)I, (T_*)ggu_out, ggu_ld, da_out, dg_out)
+    if (nj == 1) MOE_GLU_BWD_VEC(1);
+    else if (nj == 2) MOE_GLU_BWD_VEC(2);
+    else MOE_GLU_BWD_VEC(4);
+#undef MOE_GLU_BWD_VEC
+  } else {
+    MOE_BY_DTYPE(dtype, glu_bwd_kernel, dim3((unsigned)n_rows), dim3(GLU_THREADS), s,
+                 (const T_*)grad_out, go_row_stride, go_col_stride, (const T_*)gate_up, gu_ld,
+                 row_act, alpha, gamma, ap_stride, (int)I, (T_*)ggu_out, ggu_ld, da_out, dg_out);
+  }
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
