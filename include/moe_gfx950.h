@@ -158,12 +158,17 @@ int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gate_up_proj, 
  * down:    out = grad_down_proj (E,H,I): rsrc = inter (R=I), csrc = grad_eo (C=H).
  * gate_up: out = grad_gate_up_proj (E,2I,H): rsrc = hidden gathered by sorted_token (R=H),
  *          csrc = ggu (C=2I).
+ * workspace (optional, moe_token_split_workspace_size() bytes, 256-byte aligned, zero-filled
+ * once; the same workspace as the token GEMMs'): when the experts' output tiles fill at most half
+ * of the CUs, each tile's row range is split into pieces whose fp32 partials meet there and are
+ * summed in a fixed order (deterministic); the workspace is left zero. NULL: no split. Calls that
+ * share a workspace must be stream-ordered.
  * Replaces `_grouped_wgrad` (kernels/sm75/moe.py:507-532,556-561) and the per-expert
  * `ge.t() @ it`, `grad_gate_up.t() @ x_s[s:en]` (:808,821). */
 int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
                       const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R, int64_t C,
                       const int32_t* offsets, const int32_t* expert_order, int n_experts, int E_glu,
-                      void* out, void* stream);
+                      void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Down-projection dX for fused codes (0 SiLU, 1 ReLU^2) with the combine backward folded in.
  * For sorted row m of GLU expert e, token t = sorted_token[m], w = top_k_weights[sorted_flat[m]]

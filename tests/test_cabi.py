@@ -65,8 +65,8 @@ def test_gemm_entry_points_reject_bad_arguments():
     assert h.moe_grouped_down_fwd(2, fake, fake, 0, 64, 64, fake, None, 10, fake, None, 0, None) == 1
     # zero rows is a no-op success
     assert h.moe_grouped_down_fwd(2, fake, fake, 4, 64, 64, fake, None, 0, fake, None, 0, None) == 0
-    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, None, 4, 4, fake, None) == 2
-    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 64, None, 64, 64, fake, fake, 3, 4, fake, None) == 1
+    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 60, None, 64, 60, fake, None, 4, 4, fake, None, 0, None) == 2
+    assert h.moe_grouped_wgrad(2, fake, 64, None, fake, 64, None, 64, 64, fake, fake, 3, 4, fake, None, 0, None) == 1
     assert h.moe_combine_fwd(2, fake, fake, fake, fake, fake, 4, 5, fake, 10, 2, 64, 0, fake, None) == 1
     assert h.moe_glu_fwd(2, fake, 10, fake, fake, None, 1, 4, 8, fake, 8, None) == 1
     # gate-weighted intermediate: 16-bit only, H % 64 == 0, inter_out required

@@ -74,3 +74,51 @@ def test_split_matches_unsplit_is_deterministic_and_clears_counters(which):
     assert bool(ws[: n_cus * 65536 * 4].view(torch.int32).ne(0).any())
     counters = ws[n_cus * 65536 * 4:].view(torch.int32)
     assert int(counters.abs().sum()) == 0
+
+
+WG_CASES = [  # (row counts per expert, R, C, gathered rows): expert tiles <= CUs / 4, so the
+    # split runs (2 pieces per tile)
+    ([3000, 2950, 0, 3100, 2990, 3007, 2800, 3333, 2999], 768, 512, True),    # 54 tiles
+    ([700, 0, 65, 1], 256, 256, False),                                       # 4 tiles
+]
+
+
+@pytest.mark.parametrize("counts,R,C,gather", WG_CASES, ids=["stack-down", "tiny"])
+def test_wgrad_split_matches_unsplit_is_deterministic_and_clears_counters(counts, R, C, gather):
+    """moe_grouped_wgrad with the split workspace, when the experts' tiles fill at most a quarter
+    of the CUs: each tile's rows are cut into two pieces (whole 64-row steps, empty pieces for short or empty
+    experts) summed in piece order. Checked against fp32 torch, against the call without a
+    workspace (no split), run to run bitwise, counters left at zero, partial slots written."""
+    print(f"[gpu-case] wgrad split counts={counts} R={R} C={C}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    m, e = sum(counts), len(counts)
+    offs = _offsets(counts)
+    n_src = m + 17
+    rsrc = torch.randn(n_src, R, generator=g, device="cuda").bfloat16()
+    csrc = torch.randn(m, C, generator=g, device="cuda").bfloat16()
+    gat = torch.randperm(n_src, generator=g, device="cuda")[:m].int() if gather else None
+    n_ws = _lib.lib().moe_token_split_workspace_size()
+    ws = torch.zeros(n_ws, device="cuda", dtype=torch.uint8)
+
+    def run(w):
+        out = torch.full((e, C, R), float("nan"), device="cuda", dtype=torch.bfloat16)
+        _lib.call("moe_grouped_wgrad", _lib.dtype_code(torch.bfloat16), _lib.ptr(rsrc), R,
+                  _lib.ptr(gat), _lib.ptr(csrc), C, None, R, C, _lib.ptr(offs), None, e, e,
+                  _lib.ptr(out), _lib.ptr(w), w.numel() if w is not None else 0,
+                  _lib.stream_of(rsrc.device))
+        return out
+    s1, s2, plain = run(ws), run(ws), run(None)
+    torch.cuda.synchronize()
+    rows = rsrc[gat.long()] if gather else rsrc[:m]
+    s = 0
+    for x, c in enumerate(counts):
+        ref = csrc[s:s + c].float().t() @ rows[s:s + c].float()
+        d = (s1[x].float() - ref).abs()
+        assert bool(torch.isfinite(s1[x]).all())
+        assert (d <= 1e-2 * ref.abs() + 2e-2).all(), (x, d.max().item())
+        assert ((plain[x].float() - s1[x].float()).abs() <= 2 ** -7 * ref.abs() + 2e-2).all()
+        s += c
+    assert torch.equal(s1, s2)
+    n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert bool(ws[: n_cus * 65536 * 4].view(torch.int32).ne(0).any())
+    assert int(ws[n_cus * 65536 * 4:].view(torch.int32).abs().sum()) == 0

@@ -360,6 +360,11 @@ struct WgradArgs {
   const int32_t* offsets;
   int n_rtiles, n_ctiles;
   void* out;
+  // K split (ring kernel only): S pieces per tile (1 = none), workgroups b = piece * Lp + tile
+  // index; fp32 partials in split_ws (one 256x256 slot per piece), one arrival counter per tile.
+  int S, Lp;
+  float* split_ws;
+  int* split_cnt;
 };
 
 template <class C>
@@ -630,6 +635,84 @@ struct V4Shape {
 using V4Sh16 = V4Shape<f32x4, v4::TI16, v4::TJ16, 16, v4::KcLoad16>;
 using V4Sh32 = V4Shape<f32x16, v4::TI, v4::TJ, 32, v4::KcLoad>;
 
+// K-split handoff between the S pieces of one output tile (slots slot0 .. slot0 + S - 1 of the
+// split workspace, one arrival counter). Every piece stores its fp32 partial accumulators with
+// device-coherent stores (agent-scope relaxed atomic stores: written through the XCD's L2), waits
+// for them and counts itself in with a device-scope atomic; the last to arrive reads every
+// piece's partials with device-coherent loads (they miss the XCD's L2), sums them in piece order
+// (the same result whichever piece arrives last), clears the counter and returns true. No L2
+// write-back or invalidate fence: an agent-scope release / acquire fence writes back or drops the
+// whole L2 of the XCD, and with it the operands the XCD's other workgroups are streaming
+// (measured: a weight gradient split 2-way ran 2.2x slower with them). Each store and load
+// instruction of a wave covers 256 contiguous bytes.
+// TWO: the caller always splits in exactly two pieces; the last piece then adds the other's
+// partials to its own accumulators (p0 + p1 = p1 + p0 exactly, the same sum in either arrival
+// order) instead of re-reading both, which keeps the sum within the register budget.
+template <bool TWO = false, class AccV, int TI_, int TJ_>
+__device__ __forceinline__ bool split_handoff(AccV (&acc)[TI_][TJ_], float* ws, int* cnt,
+                                              int slot0, int piece, int S, char* smem) {
+  constexpr int VL = (int)(sizeof(AccV) / sizeof(float));
+  constexpr int NV = TI_ * TJ_;
+  constexpr int SLOT = NV * VL * v4::NT;
+  static_assert(SLOT == 65536, "one 256 KB slot per piece");
+  const int tid = (int)threadIdx.x;
+  // Within a slot: [wave][element][lane], so consecutive elements of a thread are 256 bytes apart
+  // (16 of them reachable from one address register with the instruction's immediate offset).
+  const int toff = (tid >> 6) * (NV * VL * 64) + (tid & 63);
+  float* mine = ws + (size_t)(slot0 + piece) * SLOT + toff;
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      __hip_atomic_store(mine + (v * VL + i) * 64, acc[v / TJ_][v % TJ_][i], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  int* s_flag = (int*)smem;  // the ring is drained and idle between the K loop and the epilogue
+  if (tid == 0)
+    *s_flag = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const bool last = *s_flag == S - 1;
+  __syncthreads();  // every wave has read the flag before the epilogue reuses the LDS
+  if (!last) return false;
+  if constexpr (TWO) {
+    const float* src = ws + (size_t)(slot0 + (piece ^ 1)) * SLOT + toff;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int i = 0; i < VL; ++i)
+        acc[v / TJ_][v % TJ_][i] += __hip_atomic_load(src + (v * VL + i) * 64, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+      // Groups of 32 loads: the sums of the group are complete at the empty asm that "modifies"
+      // its vectors, so the loads of later groups cannot be hoisted above it and pile up in
+      // registers (hoisted all together they spilled).
+      if ((v + 1) * VL % 32 == 0 || v + 1 == NV) {
+        asm volatile("" : "+v"(acc[v / TJ_][v % TJ_]));
+        if (v > 0) asm volatile("" : "+v"(acc[(v - 1) / TJ_][(v - 1) % TJ_]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int i = 0; i < VL; ++i) acc[v / TJ_][v % TJ_][i] = 0.f;
+  for (int q = 0; q < S; ++q) {
+    const float* src = ws + (size_t)(slot0 + q) * SLOT + toff;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+      for (int i = 0; i < VL; ++i)
+        acc[v / TJ_][v % TJ_][i] += __hip_atomic_load(src + (v * VL + i) * 64, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 // Phase timestamps for experiments (built only with -DMOE_PHASE_TRACE): per workgroup, the
 // 100 MHz wall clock at kernel start, K-loop start, K-loop end and epilogue end.
 #ifdef MOE_PHASE_TRACE
@@ -763,39 +846,9 @@ token_gemm_v4_kernel(TokenArgs a) {
   }
   MOE_PHASE(PH, 2);
   if (S > 1) {
-    // Split piece: every piece stores its partial tile and, after a device-scope release, counts
-    // itself in; the last to arrive acquires, sums all pieces in piece order (the same result
-    // whichever arrives last), clears the counter and runs the epilogue. Nothing waits on another
-    // workgroup.
-    f32x4* ws = (f32x4*)a.split_ws;
-    constexpr int NV = V4Sh16::TI * V4Sh16::TJ;
-#pragma unroll
-    for (int v = 0; v < NV; ++v)
-      ws[((size_t)(slot0 + piece) * NV + v) * v4::NT + threadIdx.x] = acc[v / V4Sh16::TJ][v % V4Sh16::TJ];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    int* s_flag = (int*)smem;  // the ring is idle between the K loop and the epilogue
-    // Handoff: every thread of every piece wrote its partials and ran an agent-scope release
-    // fence (L2 write-back) before the barrier; thread 0 then counts the piece in. In the last
-    // piece every thread runs its own agent-scope acquire (vector-cache invalidate) after the
-    // barrier that publishes the flag, so each thread's partial reads below are ordered after
-    // the other pieces' releases without relying on one thread's fence covering the whole CU.
-    if (threadIdx.x == 0) {
-      *s_flag = __hip_atomic_fetch_add(a.split_cnt + slot0, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    const bool last = *s_flag == S - 1;
-    __syncthreads();  // every wave has read the flag before the epilogue reuses the LDS
-    if (!last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    V4Sh16::zero(acc);
-    for (int q = 0; q < S; ++q) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        acc[v / V4Sh16::TJ][v % V4Sh16::TJ] += ws[((size_t)(slot0 + q) * NV + v) * v4::NT + threadIdx.x];
-    }
-    if (threadIdx.x == 0) a.split_cnt[slot0] = 0;
+    // Split piece: the last piece to arrive sums all pieces' partials and runs the epilogue;
+    // nothing waits on another workgroup.
+    if (!split_handoff(acc, a.split_ws, a.split_cnt + slot0, slot0, piece, S, smem)) return;
   }
   float wrow = 1.f;
   if constexpr (WGATE) {
@@ -1114,7 +1167,7 @@ token_gemm_v5_kernel(TokenArgs a) {
 
 // Weight gradients on the eight-wave ring kernel: out[e, c, r] = sum over expert e's sorted rows m
 // of rsrc[rrow(m), r] * csrc[crow(m), c]; both operands row-contiguous (optionally gathered rows).
-template <typename T, bool RG, bool CG>
+template <typename T, bool RG, bool CG, bool SPLIT>
 __global__ void __launch_bounds__(v4::NT, 1)
 wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int xr, int xc) {
   extern __shared__ __attribute__((aligned(1024))) char smem[];
@@ -1125,7 +1178,9 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
   // tile count is a multiple of 8). With xr > 0 the r x c tile grid is cut into 8 rectangles of
   // xr x xc tiles and XCD x takes rectangle x, so the tiles sharing one L2 read xr r-slices and
   // xc c-slices; otherwise tiles sharing an XCD share their r-slice (rt fastest).
-  const int lid = (int)blockIdx.x;
+  // SPLIT: a separate instantiation, so the unsplit kernel's code is the same as without it.
+  const int piece = SPLIT ? (int)blockIdx.x / a.Lp : 0;
+  const int lid = SPLIT ? (int)blockIdx.x % a.Lp : (int)blockIdx.x;
   if (lid >= n_logical) return;
   const int per_e = a.n_rtiles * a.n_ctiles;
   const int ei = lid / per_e, rem = lid % per_e;
@@ -1141,10 +1196,19 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
     ct = rem / a.n_rtiles;
     rt = rem % a.n_rtiles;
   }
-  const int k0 = a.offsets[e], k1 = a.offsets[e + 1];
+  int k0 = a.offsets[e], k1 = a.offsets[e + 1];
+  if constexpr (SPLIT) {
+    // Piece `piece` of the expert's rows: whole 64-row K steps, the last piece takes the rest;
+    // pieces past the end are empty (they add zero partials).
+    const int len = ((k1 - k0 + a.S - 1) / a.S + 63) & ~63;
+    const int kb = min(k1, k0 + piece * len);
+    k1 = min(k1, kb + len);
+    k0 = kb;
+  }
   const int r0 = rt * v4::TILE, c0 = ct * v4::TILE;
   const int wr = v4::wave_r(), wc = v4::wave_c();
 
+  // kend = the piece's end: K rows at or past it read zeros (the next piece's rows are not added).
   v4::RcLoad<RG, V4Sh32::TI, V4Sh32::FR> lp;
   lp.src = (const char*)((const T*)a.rsrc + r0);
   lp.ld = (size_t)a.r_ld * sizeof(T);
@@ -1163,6 +1227,11 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
   MOE_PHASE(PH, 1);
   v4::mainloop_ring<T>(acc, lp, lq, k0, k1, smem);
   MOE_PHASE(PH, 2);
+  if constexpr (SPLIT) {
+    // Split piece: the last piece of the tile to arrive sums the partials and runs the epilogue.
+    const int tile = e * per_e + rem;  // < E_glu * per_e, checked at launch against the slots
+    if (!split_handoff<true>(acc, a.split_ws, a.split_cnt + tile, tile * 2, piece, 2, smem)) return;
+  }
   wgrad_epilogue_v2<T, v4::WQ>(acc, a, e, r0, c0, smem, wr, wc);
 #ifdef MOE_PHASE_TRACE
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1335,8 +1404,7 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
   if (logical <= 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-  auto kern = a.r_gather ? (a.c_gather ? wgrad_v4_kernel<T, true, true> : wgrad_v4_kernel<T, true, false>)
-                         : (a.c_gather ? wgrad_v4_kernel<T, false, true> : wgrad_v4_kernel<T, false, false>);
+
   // Per-XCD rectangles (see wgrad_v4_kernel): 8 equal rectangles of xr x xc tiles with the fewest
   // slices per rectangle (xr + xc); 0 = the r-slice mapping (grids that do not split into 8).
   int xr = 0, xc = 0;
@@ -1350,8 +1418,24 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
       }
     }
   }
+  // K split in two when the expert tiles fill at most a quarter of the CUs (few experts and small
+  // weights, e.g. E = 9, H = 512, I = 768: 54 down tiles); the partials fit the token GEMMs'
+  // split workspace (one 256x256 fp32 slot per CU). Measured on that shape: down 72 -> 53 us
+  // with 2 pieces, 72 us with 4; the 108-tile gate/up gradient 92 -> 111 us with 2 pieces (more
+  // concurrent row streams than its L2 reuse absorbs), hence the quarter.
+  a.S = 1;
+  a.Lp = (int)grid;
+  const int n_cus = device_cus();
+  const int64_t glu_tiles = (int64_t)E_glu * a.n_rtiles * a.n_ctiles;
+  if (a.split_ws && n_cus >= 8 && 4 * glu_tiles <= n_cus) a.S = 2;
+  const int64_t grid_s = grid * a.S;
+  auto pick = [&]<bool SPLIT>() {
+    return a.r_gather ? (a.c_gather ? wgrad_v4_kernel<T, true, true, SPLIT> : wgrad_v4_kernel<T, true, false, SPLIT>)
+                      : (a.c_gather ? wgrad_v4_kernel<T, false, true, SPLIT> : wgrad_v4_kernel<T, false, false, SPLIT>);
+  };
+  auto kern = a.S > 1 ? pick.template operator()<true>() : pick.template operator()<false>();
   (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, v4::RING_LDSB);
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(v4::NT), v4::RING_LDSB, s, a, order, E_glu,
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid_s), dim3(v4::NT), v4::RING_LDSB, s, a, order, E_glu,
                      (int)logical, xr, xc);
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
@@ -1580,7 +1664,8 @@ extern "C" int moe_grouped_gateup_dx(int dtype, const void* ggu, const void* gat
 extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, const int32_t* r_gather,
                                  const void* csrc, int64_t c_ld, const int32_t* c_gather, int64_t R,
                                  int64_t C, const int32_t* offsets, const int32_t* expert_order,
-                                 int n_experts, int E_glu, void* out, void* stream) {
+                                 int n_experts, int E_glu, void* out, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   if (dtype != MOE_DT_F32 && dtype != MOE_DT_F16 && dtype != MOE_DT_BF16) return MOE_ERR_DTYPE;
   if (R <= 0 || C <= 0 || E_glu <= 0 || E_glu > MAX_GLU_EXPERTS || R >= (1 << 30) || C >= (1 << 30))
     return MOE_ERR_SHAPE;
@@ -1592,6 +1677,13 @@ extern "C" int moe_grouped_wgrad(int dtype, const void* rsrc, int64_t r_ld, cons
   a.rsrc = rsrc; a.r_ld = r_ld; a.r_gather = r_gather;
   a.csrc = csrc; a.c_ld = c_ld; a.c_gather = c_gather;
   a.R = (int)R; a.C = (int)C; a.offsets = offsets; a.out = out;
+  if (workspace) {
+    const int n = device_cus();
+    if (n < 8 || workspace_bytes < moe_token_split_workspace_size() || ((uintptr_t)workspace & 255))
+      return MOE_ERR_WORKSPACE;
+    a.split_ws = (float*)workspace;
+    a.split_cnt = (int*)((char*)workspace + (size_t)n * 65536 * sizeof(float));
+  }
   hipStream_t s = (hipStream_t)stream;
   auto go = [&]<typename T>() {
     if constexpr (sizeof(T) == 2) {

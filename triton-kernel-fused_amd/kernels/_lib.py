@@ -40,7 +40,7 @@ _SIGS = {
     "moe_gate_grad_parts": [_L],
     "moe_gate_grad": [_I, _P, _I, _L, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_grouped_gateup_dx": [_I, _P, _P, _I, _L, _L, _P, _P, _L, _P, _P, _S, _P],
-    "moe_grouped_wgrad": [_I, _P, _L, _P, _P, _L, _P, _L, _L, _P, _P, _I, _I, _P, _P],
+    "moe_grouped_wgrad": [_I, _P, _L, _P, _P, _L, _P, _L, _L, _P, _P, _I, _I, _P, _P, _S, _P],
     "moe_unpermute_bwd": [_I, _P, _P, _L, _P, _P, _P, _I, _I, _P, _L, _I, _L, _P, _P],
     "moe_glu_fwd": [_I, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P],
     "moe_glu_bwd": [_I, _P, _L, _L, _P, _L, _P, _P, _P, _I, _L, _L, _P, _L, _P, _P, _P],

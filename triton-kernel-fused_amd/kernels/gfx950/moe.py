@@ -308,14 +308,14 @@ class _MoEFunction(torch.autograd.Function):
                 g_dw = torch.empty_like(down_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(inter), inter_dim, None,
                           _lib.ptr(grad_eo), h, None, inter_dim, h, _lib.ptr(routing.offsets),
-                          _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw), stream,
-                          tag="down")
+                          _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw),
+                          *_lib.split_workspace(dev), stream, tag="down")
             if need_gu:
                 g_gu = torch.empty_like(gate_up_proj)
                 _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(hidden), h,
                           _lib.ptr(routing.sorted_token), _lib.ptr(ggu), two_i, None, h, two_i,
                           _lib.ptr(routing.offsets), _lib.ptr(routing.expert_order), n_exp, e_glu,
-                          _lib.ptr(g_gu), stream, tag="gate_up")
+                          _lib.ptr(g_gu), *_lib.split_workspace(dev), stream, tag="gate_up")
         elif e_glu > 0:
             if need_dw:
                 g_dw = torch.zeros_like(down_proj)
@@ -374,14 +374,14 @@ def _backward_gated(ctx, go, need_x, need_wt, need_gu, need_dw, need_ap):
         g_dw = torch.empty_like(down_proj)
         _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(inter_w), inter_dim, None, _lib.ptr(go),
                   go_ld, _lib.ptr(routing.sorted_token), inter_dim, h, _lib.ptr(routing.offsets),
-                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw), stream,
-                  tag="down")
+                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_dw),
+                  *_lib.split_workspace(dev), stream, tag="down")
     if need_gu:
         g_gu = torch.empty_like(gate_up_proj)
         _lib.call("moe_grouped_wgrad", dtc, _lib.ptr(hidden), h, _lib.ptr(routing.sorted_token),
                   _lib.ptr(ggu), 2 * inter_dim, None, h, 2 * inter_dim, _lib.ptr(routing.offsets),
-                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_gu), stream,
-                  tag="gate_up")
+                  _lib.ptr(routing.expert_order), n_exp, e_glu, _lib.ptr(g_gu),
+                  *_lib.split_workspace(dev), stream, tag="gate_up")
     if need_x:
         gxs = torch.empty(m, h, device=dev, dtype=dt)
         _lib.call("moe_grouped_gateup_dx", dtc, _lib.ptr(ggu), _lib.ptr(gate_up_proj), e_glu, h,
