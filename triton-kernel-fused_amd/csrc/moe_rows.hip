@@ -93,11 +93,11 @@ __device__ __forceinline__ int slot_kind(int64_t e, const int32_t* codes, int E_
 //   acc = sum_j g_j * row_j,  row_j = rows[f2s[t,j]] for a GLU expert (g_j = gate if GATE_GLU,
 //   else 1) or self[t] for an Identity expert (g_j = gate); Zero experts and invalid ids add
 //   nothing.
-// Column chunks per wave in the per-token gathers: two put 16 loads in flight behind one round of
-// routing reads (measured ~4% faster than one; four is level).
-constexpr int CPW = 2;
-
-template <typename T, bool GATE_GLU, int BATCH>
+// CPW (column chunks per wave): two put 16 loads in flight behind one round of routing reads
+// (measured ~4% faster than one at H = 2048; four is level); one when a row is a single chunk
+// (H <= 512 for 16-bit types). BATCH: k rounded up to 2, 4 or 8, so a small top-k does not load
+// (and discard) rows for slots that do not exist.
+template <typename T, bool GATE_GLU, int BATCH, int CPW>
 __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T* __restrict__ self,
                                              int64_t self_ld, const T* __restrict__ wt,
                                              const int64_t* __restrict__ idx,
@@ -161,13 +161,14 @@ __device__ __forceinline__ void token_gather(const T* __restrict__ rows, const T
 }
 
 // out[t] = sum_j w[t,j] * row(t,j); GATE_GLU false: GLU rows already carry their gate.
-template <typename T, bool GATE_GLU>
+template <typename T, bool GATE_GLU, int BATCH, int CPW>
 __global__ void __launch_bounds__(ROW_THREADS)
 combine_fwd_kernel(const T* __restrict__ eo, const T* __restrict__ hidden,
                    const T* __restrict__ wt, const int64_t* __restrict__ idx,
                    const int32_t* __restrict__ codes, int E_glu, int E_all,
                    const int32_t* __restrict__ f2s, int64_t N, int k, int H, T* __restrict__ out) {
-  token_gather<T, GATE_GLU, 8>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H, out);
+  token_gather<T, GATE_GLU, BATCH, CPW>(eo, hidden, H, wt, idx, codes, E_glu, E_all, f2s, N, k, H,
+                                        out);
 }
 
 // Per sorted row r (token t, flat f): grad_eo[r] = go[t]*w; grad_wt[f] = sum_h go[t,h]*row[h].
@@ -265,7 +266,7 @@ gate_grad_kernel(const float* __restrict__ part, int n_parts, int64_t n_rows,
 }
 
 // grad_x[t] = sum_j (GLU: grad_xs[pos]; Identity: w*go[t]; Zero: 0)
-template <typename T, int BATCH>
+template <typename T, int BATCH, int CPW>
 __global__ void __launch_bounds__(ROW_THREADS)
 unpermute_bwd_kernel(const T* __restrict__ gxs, const T* __restrict__ go, int64_t go_ld,
                      const T* __restrict__ wt, const int64_t* __restrict__ idx,
@@ -273,7 +274,8 @@ unpermute_bwd_kernel(const T* __restrict__ gxs, const T* __restrict__ go, int64_
                      const int32_t* __restrict__ f2s, int64_t N, int k, int H,
                      T* __restrict__ gx) {
   // GLU expert rows of grad_xs already carry the gate weight; Identity slots add w * grad_out.
-  token_gather<T, false, BATCH>(gxs, go, go_ld, wt, idx, codes, E_glu, E_all, f2s, N, k, H, gx);
+  token_gather<T, false, BATCH, CPW>(gxs, go, go_ld, wt, idx, codes, E_glu, E_all, f2s, N, k, H,
+                                     gx);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -651,11 +653,45 @@ static int glu_vec_chunks(int64_t I, int v, int max_nj) {
   return 0;
 }
 
-// Waves per token for the per-token gathers (combine, un-permute): one per 64*vec-column chunk.
-// Each wave keeps its token's 8 row loads in flight together; whole-token waves loading one row
-// at a time measured ~20% slower even when the grid alone fills the GPU.
-static int64_t token_col_waves(int64_t H, int vec) {
-  return ((H + 64 * vec - 1) / (64 * vec) + CPW - 1) / CPW;
+// Per-token gathers (combine, un-permute): CPW column chunks of 64*vec per wave, BATCH routed rows
+// loaded together. Each wave keeps its token's row loads in flight together; whole-token waves
+// loading one row at a time measured ~20% slower even when the grid alone fills the GPU.
+struct GatherCfg {
+  int batch, cpw;
+  int64_t col_waves;  // waves per token
+};
+static GatherCfg gather_cfg(int64_t H, int vec, int k) {
+  GatherCfg g;
+  const int64_t nchunk = (H + 64 * vec - 1) / (64 * vec);
+  g.batch = k <= 2 ? 2 : k <= 4 ? 4 : 8;
+  g.cpw = nchunk >= 2 ? 2 : 1;
+  g.col_waves = (nchunk + g.cpw - 1) / g.cpw;
+  return g;
+}
+// Calls f(integral_constant<BATCH>, integral_constant<CPW>) for the configuration g.
+template <class F>
+static void with_gather_cfg(const GatherCfg& g, F&& f) {
+  using B2 = std::integral_constant<int, 2>;
+  using B4 = std::integral_constant<int, 4>;
+  using B8 = std::integral_constant<int, 8>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  if (g.cpw == 1) {
+    if (g.batch == 2) f(B2{}, C1{});
+    else if (g.batch == 4) f(B4{}, C1{});
+    else f(B8{}, C1{});
+  } else {
+    if (g.batch == 2) f(B2{}, C2{});
+    else if (g.batch == 4) f(B4{}, C2{});
+    else f(B8{}, C2{});
+  }
+}
+// Calls f(T{}) with T the element type of dtype (bf16, f16 or float).
+template <class F>
+static void with_dtype(int dtype, F&& f) {
+  if (dtype == MOE_DT_BF16) f(bf16{});
+  else if (dtype == MOE_DT_F16) f(f16{});
+  else f(float{});
 }
 
 extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
@@ -670,18 +706,20 @@ extern "C" int moe_combine_fwd(int dtype, const void* eo, const void* hidden,
       (E_glu > 0 && !eo))
     return MOE_ERR_SHAPE;
   if (!al16(hidden) || !al16(out) || (eo && !al16(eo))) return MOE_ERR_ALIGN;
-  const int64_t col_waves = token_col_waves(H, vec_of(dtype));
-  if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
+  const GatherCfg gc = gather_cfg(H, vec_of(dtype), top_k);
+  if (n_tokens * gc.col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(row_grid(n_tokens * col_waves));
-  if (glu_rows_weighted)
-    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, false, grid, dim3(ROW_THREADS), s,
-                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
-  else
-    MOE_BY_DTYPE_B(dtype, combine_fwd_kernel, true, grid, dim3(ROW_THREADS), s,
-                   (const T_*)eo, (const T_*)hidden, (const T_*)top_k_weights, top_k_indices,
-                   act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k, (int)H, (T_*)out);
+  const dim3 grid(row_grid(n_tokens * gc.col_waves));
+  with_dtype(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    with_gather_cfg(gc, [&](auto b, auto c) {
+      constexpr int B = decltype(b)::value, C = decltype(c)::value;
+      auto kern = glu_rows_weighted ? combine_fwd_kernel<T, false, B, C> : combine_fwd_kernel<T, true, B, C>;
+      hipLaunchKernelGGL(kern, grid, dim3(ROW_THREADS), 0, s, (const T*)eo, (const T*)hidden,
+                         (const T*)top_k_weights, top_k_indices, act_codes, E_glu, n_experts,
+                         flat_to_sorted, n_tokens, top_k, (int)H, (T*)out);
+    });
+  });
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
@@ -753,13 +791,19 @@ extern "C" int moe_unpermute_bwd(int dtype, const void* grad_xs, const void* gra
   if (grad_out_ld < H || grad_out_ld % vec_of(dtype)) return MOE_ERR_ALIGN;
   if (!al16(grad_out) || !al16(grad_x_out) || (grad_xs && !al16(grad_xs))) return MOE_ERR_ALIGN;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t col_waves = token_col_waves(H, vec_of(dtype));
-  if (n_tokens * col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
-  const dim3 grid(row_grid(n_tokens * col_waves));
-  MOE_BY_DTYPE_B(dtype, unpermute_bwd_kernel, 8, grid, dim3(ROW_THREADS), s,
-                 (const T_*)grad_xs, (const T_*)grad_out, grad_out_ld, (const T_*)top_k_weights,
-                 top_k_indices, act_codes, E_glu, n_experts, flat_to_sorted, n_tokens, top_k,
-                 (int)H, (T_*)grad_x_out);
+  const GatherCfg gc = gather_cfg(H, vec_of(dtype), top_k);
+  if (n_tokens * gc.col_waves >= ((int64_t)1 << 32)) return MOE_ERR_SHAPE;
+  const dim3 grid(row_grid(n_tokens * gc.col_waves));
+  with_dtype(dtype, [&](auto tv) {
+    using T = decltype(tv);
+    with_gather_cfg(gc, [&](auto b, auto c) {
+      constexpr int B = decltype(b)::value, C = decltype(c)::value;
+      hipLaunchKernelGGL((unpermute_bwd_kernel<T, B, C>), grid, dim3(ROW_THREADS), 0, s,
+                         (const T*)grad_xs, (const T*)grad_out, grad_out_ld,
+                         (const T*)top_k_weights, top_k_indices, act_codes, E_glu, n_experts,
+                         flat_to_sorted, n_tokens, top_k, (int)H, (T*)grad_x_out);
+    });
+  });
   return hipGetLastError() == hipSuccess ? MOE_OK : MOE_ERR_LAUNCH;
 }
 
