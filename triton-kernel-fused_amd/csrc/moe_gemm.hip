@@ -1229,6 +1229,8 @@ wgrad_v4_kernel(WgradArgs a, const int32_t* order, int E_glu, int n_logical, int
   MOE_PHASE(PH, 2);
   if constexpr (SPLIT) {
     // Split piece: the last piece of the tile to arrive sums the partials and runs the epilogue.
+    // The launch sets a.S = 2 whenever it picks this instantiation (launch_wgrad_v2), which the
+    // two-piece handoff relies on.
     const int tile = e * per_e + rem;  // < E_glu * per_e, checked at launch against the slots
     if (!split_handoff<true>(acc, a.split_ws, a.split_cnt + tile, tile * 2, piece, 2, smem)) return;
   }
@@ -1404,7 +1406,6 @@ static int launch_wgrad_v2(WgradArgs a, const int32_t* order, int n_entries, int
   if (logical <= 0) return MOE_OK;
   const int64_t grid = (logical + 7) / 8 * 8;
   if (grid >= (int64_t)1 << 31) return MOE_ERR_SHAPE;
-
   // Per-XCD rectangles (see wgrad_v4_kernel): 8 equal rectangles of xr x xc tiles with the fewest
   // slices per rectangle (xr + xc); 0 = the r-slice mapping (grids that do not split into 8).
   int xr = 0, xc = 0;

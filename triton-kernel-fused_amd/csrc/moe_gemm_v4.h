@@ -502,8 +502,8 @@ __device__ __forceinline__ void mainloop_ring(AccV (&acc)[TI_][TJ_], LP& lp, LQ&
 // Expert lookup of token tiles from the sorted-row offsets, in scalar registers: a walk over the
 // experts that resumes where the previous lookup stopped (a workgroup's token tiles come in
 // non-decreasing order when its tile stride is a multiple of the tile group; otherwise the walk
-// steps back from where it is). The offsets are read with scalar loads (scalar cache, counted apart from the vector
-// memory operations whose waits the ring relies on).
+// steps back from where it is). The offsets are read with scalar loads (scalar cache, counted
+// apart from the vector memory operations whose waits the ring relies on).
 struct Experts {
   const int32_t* off;
   int E;
