@@ -165,3 +165,34 @@ def test_row_expert_with_dropped_ids():
     assert ra.tolist() == [2, 2, 4, 6, 6, 6, 8, 8] and rg.tolist() == [3, 3, 5, 7, 7, 7, 9, 9]
     valid = rexp2 < min(ap.shape[0], n_exp)
     assert valid.tolist() == [True] * 6 + [False] * 2
+
+
+def _header_params():
+    """name -> list of C parameter types, parsed from the declarations in the header."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|size_t|int64_t|const char\*)\s+(moe_[a-z0-9_]+)\s*\(([^)]*)\)\s*;",
+                         text):
+        args = [a.strip() for a in m.group(2).replace("\n", " ").split(",") if a.strip()]
+        if args == ["void"]:
+            args = []
+        out[m.group(1)] = [re.sub(r"\s*\b\w+$", "", a).replace(" ", "") for a in args]
+    return out
+
+
+def test_binding_argtypes_match_the_header():
+    """Every ctypes argtype list in kernels/_lib.py has the header's parameter count, and each
+    pointer / 32-bit / 64-bit / size_t / float parameter maps to the matching ctypes type."""
+    import ctypes
+    decl = _header_params()
+    assert set(decl) == set(_lib.declared_symbols())
+    kind = {ctypes.c_void_p: "p", ctypes.c_int: "i32", ctypes.c_int64: "i64", ctypes.c_size_t: "sz",
+            ctypes.c_float: "f32"}
+    for name, params in decl.items():
+        argtypes = _lib._SIGS[name]
+        assert len(argtypes) == len(params), (name, params, argtypes)
+        for c, a in zip(params, argtypes):
+            want = ("p" if "*" in c else "i32" if c in ("int", "unsignedint") else
+                    "i64" if c == "int64_t" else "sz" if c == "size_t" else "f32" if c == "float"
+                    else c)
+            assert kind[a] == want, (name, c, a)
